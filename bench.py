@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark: fused sigmoid attention fwd and fwd+bwd TFLOPS on one MI355X.
+
+Default workload (the headline config): dense bf16
+B=4 L=4096 H=16 D=128, causal, q/k/v/dO ~ N(0,1) from a seeded CPU generator,
+scale = 1/sqrt(D), default bias -log(L).  One step = forward + backward through
+the public API (`sigmoid_attention(...)` then `out.backward(dO)`), i.e. the fwd
+kernel, the dQ kernel and the dK/dV kernel, with inputs resident in HBM.
+
+FLOPs (algorithmic, extending the reference's benchmarks/benchmark_sigmoid.py
+:252-260): per (b, h) and visible (query, key) pair, fwd = 4·D, bwd = 10·D,
+fwd+bwd = 14·D; causal counts L²/2 pairs.  Recomputed or masked work is not
+credited.
+
+Prints ONE JSON line on stdout; details go to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "triton-sigmoid_amd"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+METRIC = "fwd & fwd+bwd TFLOPS + % of fp16 MFMA peak, dense/padded L=4096 D=128"
+
+CONFIGS = {
+    "c2": dict(B=2, L=1024, H=8, D=64, dtype="float16", causal=False),
+    "c2c": dict(B=2, L=1024, H=8, D=64, dtype="float16", causal=True),
+    "c3": dict(B=4, L=4096, H=16, D=128, dtype="bfloat16", causal=True),
+    "c3nc": dict(B=4, L=4096, H=16, D=128, dtype="bfloat16", causal=False),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def pairs(L: int, causal: bool) -> float:
+    return L * L / 2.0 if causal else float(L * L)
+
+
+def make_inputs(cfg, device):
+    import torch
+    dtype = getattr(torch, cfg["dtype"])
+    g = torch.Generator().manual_seed(0)
+    shape = (cfg["B"], cfg["L"], cfg["H"], cfg["D"])
+    return [torch.randn(shape, generator=g, dtype=torch.float32).to(dtype).to(device) for _ in range(4)]
+
+
+def time_region(fn, iters: int, warmup: int):
+    """Median per-call ms over `iters` calls bracketed by events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times), times
+
+
+def kernel_times(cfg, q, k, v, do, iters: int):
+    """Average duration of each kernel, launched one at a time through the C ABI
+    on torch's current stream and bracketed by HIP events on that stream."""
+    import ctypes
+    import torch
+    from triton_sigmoid import _capi
+    lib = _capi.load_library()
+    B, L, H, D = q.shape
+    bias = torch.full((B,), -math.log(L), dtype=torch.float32, device=q.device)
+    scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=q.device)
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, cfg["causal"])
+    o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    stream = torch.cuda.current_stream().cuda_stream
+    calls = {
+        "fwd": lambda: lib.sigattn_fwd(ctypes.byref(pr), o.data_ptr(), stream),
+        "bwd_dq": lambda: lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream),
+        "bwd_dkdv": lambda: lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
+                                                 dv.data_ptr(), stream),
+    }
+    out = {}
+    for name, fn in calls.items():
+        for _ in range(3):
+            assert fn() == 0
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        e.synchronize()
+        out[name] = s.elapsed_time(e) / iters
+    return out
+
+
+def cpu_baseline(cfg, budget_s: float = 20.0):
+    """fp32 eager forward + autograd backward of the oracle's restatement of the
+    reference's sigmoid_attention_ref, on the host cores, over a bounded slice
+    (first batch element, first few heads) of the same workload."""
+    import torch
+    from oracle.eager import fwd_bwd_fp32
+    torch.set_num_threads(os.cpu_count() or 1)
+    L, D, causal = cfg["L"], cfg["D"], cfg["causal"]
+    g = torch.Generator().manual_seed(0)
+    heads = 1
+    q, k, v, do = (torch.randn((1, L, heads, D), generator=g) for _ in range(4))
+    t0 = time.perf_counter()
+    fwd_bwd_fp32(q, k, v, do, causal=causal)  # warm-up
+    one = time.perf_counter() - t0
+    heads = max(1, min(cfg["H"], int(budget_s / 3.0 / max(one, 1e-3))))
+    q, k, v, do = (torch.randn((1, L, heads, D), generator=g) for _ in range(4))
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fwd_bwd_fp32(q, k, v, do, causal=causal)
+        runs.append(time.perf_counter() - t0)
+    t = statistics.median(runs)
+    flops = 14 * D * pairs(L, causal) * heads
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"fp32 eager fwd+bwd (oracle/eager.py) on B=1 H={heads} of the same L={L} D={D} "
+                  f"causal={causal} workload, median of 3 after 1 warm-up, {t:.2f} s each",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every (batch, head) pair is independent; sharding is described in DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import triton_sigmoid as ts
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    q, k, v, do = make_inputs(cfg, dev)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    B, L, H, D, causal = cfg["B"], cfg["L"], cfg["H"], cfg["D"], cfg["causal"]
+    P = pairs(L, causal) * B * H
+    fwd_flops, fb_flops = 4 * D * P, 14 * D * P
+
+    def fwd():
+        with torch.no_grad():
+            ts.sigmoid_attention(q, k, v, is_causal=causal)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        o = ts.sigmoid_attention(q, k, v, is_causal=causal)
+        o.backward(do)
+
+    # Whole-job timing of K fwd+bwd steps.
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    fb_tflops = fb_flops / (ms_step * 1e-3) / 1e12
+
+    fwd_ms, _ = time_region(fwd, iters=max(10, args.steps), warmup=3)
+    fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
+    kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, args.steps))
+    credit = {"fwd": 4 * D * P, "bwd_dq": 2 * D * P, "bwd_dkdv": 8 * D * P}
+    dominant = max(kt, key=kt.get)
+    achieved = credit[dominant] / (kt[dominant] * 1e-3) / 1e12
+    bwd_ms = kt["bwd_dq"] + kt["bwd_dkdv"]
+    log(f"[bench] config={args.config} {cfg}")
+    log(f"[bench] step {ms_step:.3f} ms -> fwd+bwd {fb_tflops:.1f} TFLOPS ({100 * fb_tflops / PEAK_BF16_TFLOPS:.1f}% peak)")
+    log(f"[bench] fwd {fwd_ms:.3f} ms -> {fwd_tflops:.1f} TFLOPS; kernels (ms): "
+        + ", ".join(f"{n}={t:.3f}" for n, t in kt.items()))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg)
+        log(f"[bench] cpu baseline {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(fb_tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg["dtype"] == "bfloat16" else "fp16",
+        "data": "synthetic: q,k,v,dO ~ N(0,1) from torch.Generator seed 0",
+        "config": {
+            "workload": f"dense sigmoid attention fwd+bwd, B={B} L={L} H={H} D={D} "
+                        f"{cfg['dtype']} causal={causal} (BASELINE.json configs[2])" if args.config == "c3"
+                        else f"dense sigmoid attention fwd+bwd, B={B} L={L} H={H} D={D} {cfg['dtype']} causal={causal}",
+            "batch": B, "seq_len": L, "heads": H, "head_dim": D, "causal": causal,
+        },
+        "pct_of_peak": round(100 * fb_tflops / PEAK_BF16_TFLOPS, 2),
+        "fwd_tflops": round(fwd_tflops, 2),
+        "fwd_pct_of_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
+        "bwd_only_tflops": round(10 * D * P / (bwd_ms * 1e-3) / 1e12, 2),
+        "kernel_ms": {n: round(t, 4) for n, t in kt.items()},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+/*
+ * sigattn.h — C ABI of the MI355X (gfx950) fused sigmoid-attention library
+ * (libsigattn.so).
+ *
+ *   O = sigmoid(Q·Kᵀ·scale + bias[b] + score_mod[b, key]) · V
+ *
+ * with optional top-left causal masking (key <= query) and right padding
+ * (only the first seq_lens_q[b] queries / seq_lens_k[b] keys of batch b are
+ * valid), plus the recompute backward (dQ, dK, dV).  Tensors are [B, T, H, D]
+ * with unit stride along D.  All pointers are device pointers; nothing here
+ * allocates, synchronises the host or throws across the ABI.
+ *
+ * These entry points replace the kernel launches inside the reference's four
+ * torch.library ops (MSDLLCpapers/triton-sigmoid, src/triton_sigmoid/):
+ *   sigattn_fwd  <- sigmoid_triton_dense.py:534-560   (_fwd_dense_kernel launch)
+ *                <- sigmoid_triton_padded.py:591-621  (_fwd_padded_kernel launch)
+ *   sigattn_bwd  <- sigmoid_triton_dense.py:630-686   (dQ + dK/dV launches)
+ *                <- sigmoid_triton_padded.py:706-770  (dQ + dK/dV launches)
+ * The Python op layer (torch.library custom ops with the reference's names
+ * and schemas) calls them through ctypes with torch's current HIP stream.
+ */
+#ifndef SIGATTN_H
+#define SIGATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIGATTN_ABI_VERSION 1
+
+/* Element type of Q, K, V, dO and of every output. */
+enum sigattn_dtype {
+  SIGATTN_F16 = 0,
+  SIGATTN_BF16 = 1,
+  SIGATTN_F32 = 2
+};
+
+/* Return codes: 0 on success, negative on error (see sigattn_strerror). */
+enum sigattn_status {
+  SIGATTN_OK = 0,
+  SIGATTN_ERR_NULL_ARG = -1,      /* a required pointer is NULL */
+  SIGATTN_ERR_DTYPE = -2,         /* dtype code not in enum sigattn_dtype */
+  SIGATTN_ERR_HEAD_DIM = -3,      /* D not in {16, 32, 64, 128} */
+  SIGATTN_ERR_SHAPE = -4,         /* negative size, or B*H / T too large */
+  SIGATTN_ERR_STRIDE = -5,        /* negative stride */
+  SIGATTN_ERR_DENSE_LENGTHS = -6, /* dense call (no seq_lens) with Tq != Tk */
+  SIGATTN_ERR_ABI_VERSION = -7,   /* problem.abi_version != SIGATTN_ABI_VERSION */
+  SIGATTN_ERR_LAUNCH = -8         /* hipGetLastError() reported a failure */
+};
+
+/*
+ * One attention problem.  Strides are in elements; the D stride is 1.
+ * Q, O, dO and dQ share the q_stride_* layout; K, V, dK and dV share the
+ * k_stride_* layout (the reference passes exactly these two stride sets to
+ * every kernel: sigmoid_triton_dense.py:505-506).
+ */
+typedef struct sigattn_problem {
+  int32_t abi_version;    /* must be SIGATTN_ABI_VERSION */
+  int32_t dtype;          /* enum sigattn_dtype */
+  int64_t B, Tq, Tk, H, D;
+  int64_t q_stride_b, q_stride_t, q_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  const void *q;          /* [B, Tq, H, D] */
+  const void *k;          /* [B, Tk, H, D] */
+  const void *v;          /* [B, Tk, H, D] */
+  const float *bias;      /* [B] fp32, added after the scale */
+  const float *scale;     /* 0-d fp32 device scalar (read by the kernels) */
+  const float *score_mod; /* [B, Tk] fp32 contiguous, or NULL */
+  const int32_t *seq_lens_q; /* [B] int32 or NULL; NULL with seq_lens_k NULL = dense */
+  const int32_t *seq_lens_k; /* [B] int32 or NULL */
+  int32_t causal;         /* nonzero: key index <= query index (top-left) */
+} sigattn_problem;
+
+/* ABI version compiled into the library. */
+int sigattn_abi_version(void);
+
+/* Human-readable text for a status code (static storage). */
+const char *sigattn_strerror(int status);
+
+/* Validates a problem without touching the GPU (0 or a negative status). */
+int sigattn_check(const sigattn_problem *p);
+
+/*
+ * Forward: out[B, Tq, H, D] (q strides).  Rows at or past seq_lens_q[b] are
+ * written as zeros.  `stream` is a hipStream_t (NULL = default stream).
+ */
+int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
+
+/*
+ * Recompute backward: dq (q strides), dk and dv (k strides) from dout
+ * (q strides).  No atomics: results are bitwise deterministic.  Padded query
+ * rows get dq = 0, padded key rows get dk = dv = 0.
+ */
+int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
+                void *dv, void *stream);
+
+/*
+ * The two halves of sigattn_bwd, one kernel each (the reference launches the
+ * dQ kernel and the dK/dV kernel separately: sigmoid_triton_dense.py:630-656
+ * and :659-686).  Used to time the kernels one at a time.
+ */
+int sigattn_bwd_dq(const sigattn_problem *p, const void *dout, void *dq, void *stream);
+int sigattn_bwd_dkdv(const sigattn_problem *p, const void *dout, void *dk, void *dv,
+                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIGATTN_H */

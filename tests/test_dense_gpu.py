@@ -1,0 +1,230 @@
+"""GPU parity tests for the dense path (sigmoid_attention -> myops::sigmoid_attention_fwd/bwd
+-> libsigattn.so).  Mirrors the reference's tests/test_sigmoid_dense.py."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import triton_sigmoid as ts
+from conftest import get_tolerance
+from helpers import assert_close_to_oracle, oracle_fwd_bwd, randn
+from oracle.eager import sigmoid_attention_eager
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+
+
+def _inputs(B, T, H, D, dtype, seed=0, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [randn((B, T, H, D), dtype, DEV, g, std) for _ in range(4)]
+
+
+# --- tight parity against the float64 oracle (odd sizes, every head dim) -------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("T", [1, 17, 130, 300])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_matches_oracle(dtype, D, T, causal):
+    B, H = 2, 3
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=T * 7 + D)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=causal)
+    o.backward(do)
+    scale = 1.0 / math.sqrt(D)
+    bias = np.full(B, -math.log(T), dtype=np.float32).astype(np.float64)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(scale), bias=bias, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_score_mod_matches_oracle(dtype, D, causal):
+    B, T, H = 2, 200, 2
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=11)
+    g = torch.Generator().manual_seed(5)
+    sm = torch.randn((B, T), generator=g).to(dtype).to(DEV)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=causal, score_mod=sm, sigmoid_bias=-2.0, scale=0.1)
+    o.backward(do)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(0.1), bias=np.full(B, -2.0),
+                                          score_mod=sm, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
+# --- the reference's own criterion (tests/test_sigmoid_dense.py:35-166) -------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,H", [(1, 2), (4, 8)])
+@pytest.mark.parametrize("T", [128, 1024, 4096])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_reference_criterion(dtype, B, H, T, D, causal):
+    if dtype == torch.float32 and T == 4096 and B == 4:
+        pytest.skip("fp32 takes the portable kernel; the large fp32 case only adds run time")
+    tol = get_tolerance(dtype)
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=B + T + D, std=0.5)
+    do = do.float() * 2.0  # N(0, 1) like torch.randn_like(out) in the reference test
+    leaves = {}
+    outs = {}
+    for name in ("ref", "pt", "ours"):
+        leaves[name] = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+    outs["ref"] = sigmoid_attention_eager(*leaves["ref"], upcast=True, causal=causal)
+    outs["pt"] = sigmoid_attention_eager(*leaves["pt"], upcast=False, reorder_ops=True, causal=causal)
+    outs["ours"] = ts.sigmoid_attention(*leaves["ours"], is_causal=causal)
+    err = (outs["ours"].float() - outs["ref"].float()).abs().max().item()
+    err_pt = (outs["pt"].float() - outs["ref"].float()).abs().max().item()
+    assert err <= 2 * err_pt + tol, (err, err_pt)
+    assert err < tol, err
+    for name in outs:
+        outs[name].backward(do.to(outs[name].dtype))
+    for i, gname in enumerate("qkv"):
+        ref_g = leaves["ref"][i].grad.float()
+        e = (leaves["ours"][i].grad.float() - ref_g).abs().max().item()
+        e_pt = (leaves["pt"][i].grad.float() - ref_g).abs().max().item()
+        assert e <= 3 * e_pt + tol, (gname, e, e_pt)
+        assert e < tol, (gname, e)
+
+
+# --- BASELINE parity bar: max-abs <= 2e-2 vs fp32 eager at N(0,1) --------------
+
+def _fp32_reference(q, k, v, do, causal, chunk_b=1):
+    outs, gq, gk, gv = [], [], [], []
+    for b0 in range(0, q.shape[0], chunk_b):
+        sl = slice(b0, b0 + chunk_b)
+        qq, kk, vv = (t[sl].detach().float().requires_grad_(True) for t in (q, k, v))
+        o = sigmoid_attention_eager(qq, kk, vv, causal=causal, upcast=True)
+        o.backward(do[sl].float())
+        outs.append(o.detach())
+        gq.append(qq.grad)
+        gk.append(kk.grad)
+        gv.append(vv.grad)
+        del o, qq, kk, vv
+    return torch.cat(outs), torch.cat(gq), torch.cat(gk), torch.cat(gv)
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(B=2, T=1024, H=8, D=64, dtype=torch.float16, causal=False),
+    dict(B=2, T=1024, H=8, D=64, dtype=torch.float16, causal=True),
+    dict(B=4, T=4096, H=16, D=128, dtype=torch.bfloat16, causal=True),
+], ids=["c2-noncausal", "c2-causal", "c3-headline"])
+def test_baseline_configs_within_2e2(cfg):
+    B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["D"]
+    q, k, v, do = _inputs(B, T, H, D, cfg["dtype"], seed=0)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=cfg["causal"])
+    o.backward(do)
+    ro, rq, rk, rv = _fp32_reference(q, k, v, do, cfg["causal"])
+    for name, got, want in (("O", o, ro), ("dQ", q.grad, rq), ("dK", k.grad, rk), ("dV", v.grad, rv)):
+        err = (got.float() - want).abs().max().item()
+        assert err <= 2e-2, (name, err)
+
+
+# --- behaviour -----------------------------------------------------------------
+
+def test_causal_past_outputs_ignore_future_keys():
+    B, T, H, D = 1, 512, 2, 128
+    q, k, v, _ = _inputs(B, T, H, D, torch.bfloat16, seed=3)
+    o1 = ts.sigmoid_attention(q, k, v, is_causal=True)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, 300:] = torch.randn_like(k2[:, 300:])
+    v2[:, 300:] = torch.randn_like(v2[:, 300:])
+    o2 = ts.sigmoid_attention(q, k2, v2, is_causal=True)
+    assert torch.equal(o1[:, :300], o2[:, :300])
+    assert not torch.equal(o1[:, 300:], o2[:, 300:])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_forward_and_backward_are_bitwise_deterministic(dtype):
+    B, T, H, D = 2, 640, 4, 64
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=4)
+    res = []
+    for _ in range(2):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        o = ts.sigmoid_attention(*leaves, is_causal=True)
+        o.backward(do)
+        res.append([o.detach()] + [t.grad for t in leaves])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_score_mod_zero_equals_none_and_constant_equals_bias():
+    B, T, H, D = 2, 256, 2, 64
+    q, k, v, _ = _inputs(B, T, H, D, torch.float16, seed=6)
+    a = ts.sigmoid_attention(q, k, v)
+    b = ts.sigmoid_attention(q, k, v, score_mod=torch.zeros(B, T, device=DEV))
+    assert torch.equal(a, b)
+    c = ts.sigmoid_attention(q, k, v, sigmoid_bias=-3.0, score_mod=torch.full((B, T), 1.0, device=DEV))
+    d = ts.sigmoid_attention(q, k, v, sigmoid_bias=-2.0)
+    torch.testing.assert_close(c, d, atol=2e-3, rtol=0)
+
+
+def test_non_contiguous_inputs():
+    B, T, H, D = 2, 200, 4, 64
+    base = torch.randn(B, H, T, D, device=DEV, dtype=torch.bfloat16)
+    q = base.transpose(1, 2)  # [B, T, H, D] view, not contiguous
+    assert not q.is_contiguous()
+    o = ts.sigmoid_attention(q, q, q)
+    o2 = ts.sigmoid_attention(q.contiguous(), q.contiguous(), q.contiguous())
+    assert torch.equal(o, o2)
+
+
+def test_large_inputs_give_finite_gradients():
+    B, T, H, D = 1, 256, 2, 64
+    q, k, v, do = _inputs(B, T, H, D, torch.float16, seed=8)
+    q, k, v = (t * 10 for t in (q, k, v))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v)
+    o.backward(do)
+    for t in (o, q.grad, k.grad, v.grad):
+        assert torch.isfinite(t).all()
+        assert t.abs().max() < 1e6
+
+
+def test_zero_inputs():
+    B, T, H, D = 1, 128, 2, 64
+    z = torch.zeros(B, T, H, D, device=DEV, dtype=torch.float16, requires_grad=True)
+    o = ts.sigmoid_attention(z, z, z)
+    assert torch.equal(o, torch.zeros_like(o))
+    o.sum().backward()
+    assert torch.isfinite(z.grad).all()
+
+
+def test_requires_grad_subsets():
+    B, T, H, D = 1, 64, 2, 64
+    q, k, v, do = _inputs(B, T, H, D, torch.bfloat16, seed=9)
+    q.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v)
+    o.backward(do)
+    assert q.grad is not None and k.grad is None and v.grad is None
+
+
+def test_empty_batch_and_length():
+    for shape in [(0, 16, 2, 64), (2, 0, 2, 64)]:
+        x = torch.randn(*shape, device=DEV, dtype=torch.float16)
+        o = ts.sigmoid_attention(x, x, x)
+        assert o.shape == x.shape
+
+
+@pytest.mark.parametrize("T", [1, 7, 15, 33])
+def test_tiny_sequence_lengths(T):
+    B, H, D = 2, 2, 64
+    q, k, v, do = _inputs(B, T, H, D, torch.float16, seed=T)
+    o = ts.sigmoid_attention(q, k, v, is_causal=True)
+    want, _ = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1 / math.sqrt(D)),
+                             bias=np.full(B, np.float32(-math.log(T))), causal=True, with_bwd=False)
+    assert_close_to_oracle(o, want, torch.float16, "O")

@@ -1,0 +1,154 @@
+"""GPU parity tests for the padded path (sigmoid_attention_padded ->
+myops::sigmoid_attn_padded_fwd/bwd -> libsigattn.so).  Mirrors the reference's
+tests/test_sigmoid_padded.py."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import triton_sigmoid as ts
+from conftest import get_tolerance
+from helpers import assert_close_to_oracle, oracle_fwd_bwd, randn, to_np
+from oracle.eager import sigmoid_attention_eager
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+
+
+def _case(B, Tq, Tk, H, D, dtype, seed, std=1.0, noise=True, lo=0.5):
+    g = torch.Generator().manual_seed(seed)
+    q = randn((B, Tq, H, D), dtype, DEV, g, std)
+    k = randn((B, Tk, H, D), dtype, DEV, g, std)
+    v = randn((B, Tk, H, D), dtype, DEV, g, std)
+    do = randn((B, Tq, H, D), dtype, DEV, g, 1.0)
+    sq = torch.randint(int(lo * Tq), Tq + 1, (B,), generator=g, dtype=torch.int32)
+    sk = sq.clone() if Tq == Tk else torch.randint(int(lo * Tk), Tk + 1, (B,), generator=g, dtype=torch.int32)
+    if noise:  # padding rows hold NaN: they must never be read
+        for b in range(B):
+            q[b, sq[b]:] = float("nan")
+            do[b, sq[b]:] = float("nan")
+            k[b, sk[b]:] = float("nan")
+            v[b, sk[b]:] = float("nan")
+    return q, k, v, do, sq.to(DEV), sk.to(DEV)
+
+
+def _clean(t, lens):
+    t = t.detach().clone()
+    for b in range(t.shape[0]):
+        t[b, int(lens[b]):] = 0
+    return t
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [16, 64, 128])
+@pytest.mark.parametrize("Tq,Tk", [(128, 128), (200, 77), (77, 300), (513, 513)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_matches_oracle(dtype, D, Tq, Tk, causal):
+    B, H = 3, 2
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=Tq + Tk + D)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal)
+    o.backward(do)
+    bias = (-torch.log(sk.float())).double().cpu().numpy()
+    qc, kc, vc, doc = _clean(q, sq), _clean(k, sk), _clean(v, sk), _clean(do, sq)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(qc, kc, vc, doc, scale=np.float32(1 / math.sqrt(D)), bias=bias,
+                                          seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+    # padded rows are exact zeros
+    for b in range(B):
+        assert torch.all(o[b, sq[b]:] == 0) and torch.all(q.grad[b, sq[b]:] == 0)
+        assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_reference_criterion(dtype, causal):
+    """tests/test_sigmoid_padded.py:48-186 criterion with seq_lens ~ U[0.8T, T]."""
+    B, T, H, D = 4, 1024, 4, 128
+    tol = get_tolerance(dtype)
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=21, std=0.5, noise=False, lo=0.8)
+    leaves = {n: [t.detach().clone().requires_grad_(True) for t in (q, k, v)] for n in ("ref", "pt", "ours")}
+    outs = {
+        "ref": sigmoid_attention_eager(*leaves["ref"], seq_lens_k=sk, seq_lens_q=sq, upcast=True, causal=causal),
+        "pt": sigmoid_attention_eager(*leaves["pt"], seq_lens_k=sk, seq_lens_q=sq, upcast=False,
+                                      reorder_ops=True, causal=causal),
+        "ours": ts.sigmoid_attention_padded(*leaves["ours"], seq_lens_k=sk, seq_lens_q=sq, is_causal=causal),
+    }
+    err = (outs["ours"].float() - outs["ref"].float()).abs().max().item()
+    err_pt = (outs["pt"].float() - outs["ref"].float()).abs().max().item()
+    assert err <= 2 * err_pt + tol and err < tol, (err, err_pt)
+    for n in outs:
+        outs[n].backward(do)
+    for i, gname in enumerate("qkv"):
+        ref_g = leaves["ref"][i].grad.float()
+        e = (leaves["ours"][i].grad.float() - ref_g).abs().max().item()
+        e_pt = (leaves["pt"][i].grad.float() - ref_g).abs().max().item()
+        assert e <= 3 * e_pt + tol and e < tol, (gname, e, e_pt)
+
+
+def test_padding_noise_invariance():
+    B, T, H, D = 2, 300, 2, 64
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.bfloat16, seed=3, noise=False)
+    a = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    for b in range(B):
+        q2[b, sq[b]:] = 1e4
+        k2[b, sk[b]:] = float("inf")
+        v2[b, sk[b]:] = float("nan")
+    b_ = ts.sigmoid_attention_padded(q2, k2, v2, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
+    assert torch.equal(a, b_)
+
+
+def test_full_lengths_match_dense():
+    B, T, H, D = 2, 384, 4, 128
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (randn((B, T, H, D), torch.bfloat16, DEV, g) for _ in range(3))
+    for causal in (False, True):
+        # Same explicit bias: the same kernel runs, so results are bitwise equal.
+        a = ts.sigmoid_attention(q, k, v, is_causal=causal, sigmoid_bias=-4.5)
+        b = ts.sigmoid_attention_padded(q, k, v, is_causal=causal, sigmoid_bias=-4.5)
+        assert torch.equal(a, b)
+        # Default biases: -log(T) in fp64 (dense) vs -log(seq_lens) in fp32
+        # (padded) may differ by one fp32 ulp (tests/test_sigmoid_padded.py:723-749
+        # compares these within 2*tol).
+        a = ts.sigmoid_attention(q, k, v, is_causal=causal)
+        b = ts.sigmoid_attention_padded(q, k, v, is_causal=causal)
+        torch.testing.assert_close(a, b, atol=2 * 7e-3, rtol=0)
+
+
+def test_zero_and_out_of_range_seq_lens():
+    B, T, H, D = 3, 128, 2, 64
+    q, k, v, do, _, _ = _case(B, T, T, H, D, torch.float16, seed=4, noise=False)
+    sq = torch.tensor([0, -5, 500], dtype=torch.int32, device=DEV)
+    sk = torch.tensor([64, 0, 1000], dtype=torch.int64, device=DEV)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, sigmoid_bias=-1.0)
+    o.backward(do)
+    assert torch.isfinite(o).all() and torch.isfinite(q.grad).all()
+    assert torch.all(o[0] == 0) and torch.all(o[1] == 0)
+    full = ts.sigmoid_attention_padded(q[2:], k[2:], v[2:], sigmoid_bias=-1.0)
+    assert torch.equal(o[2:], full)
+
+
+def test_cross_attention_short_queries():
+    B, Tq, Tk, H, D = 2, 32, 512, 2, 64
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, torch.float16, seed=5, noise=False)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq)
+    want, _ = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1 / 8), bias=(-torch.log(sk.float())).double().cpu().numpy(),
+                             seq_lens_q=sq, seq_lens_k=sk, with_bwd=False)
+    assert_close_to_oracle(o, want, torch.float16, "O")
+
+
+def test_padded_forward_deterministic():
+    q, k, v, do, sq, sk = _case(2, 700, 700, 4, 128, torch.bfloat16, seed=6, noise=False)
+    a = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
+    b = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
+    assert torch.equal(a, b)

@@ -1,0 +1,176 @@
+// C ABI of libsigattn.so (declared in include/sigattn.h).
+//
+// Validation runs on the host before any HIP call, so every error path is
+// testable without a GPU.  Dispatch: f16/bf16 with D in {64, 128} and 16-byte
+// aligned rows take the MFMA kernels; everything else takes the portable
+// kernels.  Launches are asynchronous on the caller's stream; nothing here
+// allocates or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "../../include/sigattn.h"
+#include "launch.h"
+
+using sigattn::KParams;
+
+namespace {
+
+bool is_pow2_head_dim(int64_t D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+KParams make_params(const sigattn_problem *p) {
+  KParams k{};
+  k.q = p->q;
+  k.k = p->k;
+  k.v = p->v;
+  k.bias = p->bias;
+  k.scale = p->scale;
+  k.score_mod = p->score_mod;
+  k.seq_q = p->seq_lens_q;
+  k.seq_k = p->seq_lens_k;
+  k.sq_b = p->q_stride_b;
+  k.sq_t = p->q_stride_t;
+  k.sq_h = p->q_stride_h;
+  k.sk_b = p->k_stride_b;
+  k.sk_t = p->k_stride_t;
+  k.sk_h = p->k_stride_h;
+  k.B = (int)p->B;
+  k.H = (int)p->H;
+  k.Tq = (int)p->Tq;
+  k.Tk = (int)p->Tk;
+  return k;
+}
+
+// True when the MFMA kernels can take the problem: 16-bit elements, D of 64
+// or 128, and every row start 16-byte aligned.
+bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
+  if (p->dtype == SIGATTN_F32) return false;
+  if (p->D != 64 && p->D != 128) return false;
+  const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
+                              p->k_stride_b, p->k_stride_t, p->k_stride_h};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return false;
+  for (int i = 0; i < nptr; ++i)
+    if (ptrs[i] && !aligned16(ptrs[i])) return false;
+  return true;
+}
+
+int launch_status() {
+  return hipGetLastError() == hipSuccess ? SIGATTN_OK : SIGATTN_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sigattn_abi_version(void) { return SIGATTN_ABI_VERSION; }
+
+const char *sigattn_strerror(int status) {
+  switch (status) {
+    case SIGATTN_OK: return "success";
+    case SIGATTN_ERR_NULL_ARG: return "a required pointer argument is NULL";
+    case SIGATTN_ERR_DTYPE: return "unsupported dtype code (expected f16, bf16 or f32)";
+    case SIGATTN_ERR_HEAD_DIM: return "unsupported head dimension (expected 16, 32, 64 or 128)";
+    case SIGATTN_ERR_SHAPE: return "invalid or too large problem shape";
+    case SIGATTN_ERR_STRIDE: return "invalid (negative) stride";
+    case SIGATTN_ERR_DENSE_LENGTHS:
+      return "dense attention (no seq_lens) requires the same sequence length for Q and K";
+    case SIGATTN_ERR_ABI_VERSION: return "sigattn_problem.abi_version does not match the library";
+    case SIGATTN_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown sigattn status";
+  }
+}
+
+int sigattn_check(const sigattn_problem *p) {
+  if (p == nullptr) return SIGATTN_ERR_NULL_ARG;
+  if (p->abi_version != SIGATTN_ABI_VERSION) return SIGATTN_ERR_ABI_VERSION;
+  if (p->dtype != SIGATTN_F16 && p->dtype != SIGATTN_BF16 && p->dtype != SIGATTN_F32)
+    return SIGATTN_ERR_DTYPE;
+  if (!is_pow2_head_dim(p->D)) return SIGATTN_ERR_HEAD_DIM;
+  if (p->B < 0 || p->Tq < 0 || p->Tk < 0 || p->H < 0) return SIGATTN_ERR_SHAPE;
+  if (p->Tq > (INT_MAX / 2) || p->Tk > (INT_MAX / 2) || p->B > INT_MAX || p->H > INT_MAX)
+    return SIGATTN_ERR_SHAPE;
+  // Largest grid any kernel launches: ceil(T / 64) row blocks per (b, h).
+  const int64_t rows = p->Tq > p->Tk ? p->Tq : p->Tk;
+  if (p->B * p->H > 0 && cdiv(rows, 64) > (int64_t)INT_MAX / (p->B * p->H)) return SIGATTN_ERR_SHAPE;
+  const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
+                              p->k_stride_b, p->k_stride_t, p->k_stride_h};
+  for (int64_t s : strides)
+    if (s < 0) return SIGATTN_ERR_STRIDE;
+  if (p->seq_lens_q == nullptr && p->seq_lens_k == nullptr && p->Tq != p->Tk)
+    return SIGATTN_ERR_DENSE_LENGTHS;
+  if (p->B == 0 || p->H == 0) return SIGATTN_OK;
+  if (p->bias == nullptr || p->scale == nullptr) return SIGATTN_ERR_NULL_ARG;
+  if (p->Tq > 0 && p->q == nullptr) return SIGATTN_ERR_NULL_ARG;
+  if (p->Tk > 0 && (p->k == nullptr || p->v == nullptr)) return SIGATTN_ERR_NULL_ARG;
+  return SIGATTN_OK;
+}
+
+int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
+  const int rc = sigattn_check(p);
+  if (rc != SIGATTN_OK) return rc;
+  if (p->B == 0 || p->H == 0 || p->Tq == 0) return SIGATTN_OK;
+  if (out == nullptr) return SIGATTN_ERR_NULL_ARG;
+  KParams k = make_params(p);
+  k.out = out;
+  const hipStream_t st = (hipStream_t)stream;
+  const void *ptrs[4] = {p->q, p->k, p->v, out};
+  (void)hipGetLastError();
+  if (use_mfma(p, ptrs, 4))
+    sigattn::launch_fwd_mfma(k, p->dtype, (int)p->D, p->causal != 0, p->score_mod != nullptr, st);
+  else
+    sigattn::launch_fwd_generic(k, p->dtype, (int)p->D, p->causal != 0, st);
+  return launch_status();
+}
+
+static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                    void *stream, bool do_dq, bool do_dkdv) {
+  const int rc = sigattn_check(p);
+  if (rc != SIGATTN_OK) return rc;
+  if (p->B == 0 || p->H == 0) return SIGATTN_OK;
+  const bool need_dq = do_dq && p->Tq > 0;
+  const bool need_dkdv = do_dkdv && p->Tk > 0;
+  if (need_dq && dq == nullptr) return SIGATTN_ERR_NULL_ARG;
+  if (need_dkdv && (dk == nullptr || dv == nullptr)) return SIGATTN_ERR_NULL_ARG;
+  if ((need_dq || need_dkdv) && p->Tq > 0 && dout == nullptr) return SIGATTN_ERR_NULL_ARG;
+  KParams k = make_params(p);
+  k.dout = dout;
+  k.dq = dq;
+  k.dk = dk;
+  k.dv = dv;
+  const hipStream_t st = (hipStream_t)stream;
+  const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
+  const bool mfma = use_mfma(p, ptrs, 7);
+  const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
+  (void)hipGetLastError();
+  if (need_dq) {
+    if (mfma) sigattn::launch_bwd_dq_mfma(k, p->dtype, (int)p->D, causal, sm, st);
+    else sigattn::launch_bwd_dq_generic(k, p->dtype, (int)p->D, causal, st);
+  }
+  if (need_dkdv) {
+    if (mfma) sigattn::launch_bwd_dkdv_mfma(k, p->dtype, (int)p->D, causal, sm, st);
+    else sigattn::launch_bwd_dkdv_generic(k, p->dtype, (int)p->D, causal, st);
+  }
+  return launch_status();
+}
+
+int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                void *stream) {
+  return bwd_impl(p, dout, dq, dk, dv, stream, true, true);
+}
+
+int sigattn_bwd_dq(const sigattn_problem *p, const void *dout, void *dq, void *stream) {
+  return bwd_impl(p, dout, dq, nullptr, nullptr, stream, true, false);
+}
+
+int sigattn_bwd_dkdv(const sigattn_problem *p, const void *dout, void *dk, void *dv,
+                     void *stream) {
+  return bwd_impl(p, dout, nullptr, dk, dv, stream, false, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,184 @@
+// Shared device-side definitions for the gfx950 sigmoid-attention kernels.
+//
+// MFMA tiling used by every fast kernel (v_mfma_f32_32x32x16_{bf16,f16}):
+//   * A operand: lane l holds row (l % 32), eight k-elements (k-slot h = l / 32).
+//   * B operand: lane l holds column (l % 32), eight k-elements (k-slot h).
+//     A and B use the same (h, j) -> k mapping, so any product whose two
+//     operands are both read from memory may choose that mapping freely; we use
+//     k = 8h + j (16 contiguous bytes per lane).
+//   * C/D (16 fp32 per lane): lane l holds column (l % 32), register i holds
+//     row 8*(i/4) + 4*(l/32) + (i%4).
+// A score tile computed as Sᵀ (rows = keys, columns = queries) therefore already
+// sits in the B-operand layout of the next product over keys: register group
+// i in [8s, 8s+8) of a 32-key block is B k-step s with key = 16s' + 8(j/4) +
+// 4h + (j%4).  The matching A operand (e.g. Vᵀ rows) is read from LDS with the
+// same key permutation as two 8-byte reads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sigattn {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// log2(e): sigmoid(x) = 1 / (1 + 2^(-x * log2(e))).
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Kernel parameters (passed by value).  Strides are in elements.
+struct KParams {
+  const void *q, *k, *v, *dout;
+  void *out, *dq, *dk, *dv;
+  const float *bias;       // [B]
+  const float *scale;      // 0-d
+  const float *score_mod;  // [B, Tk] fp32 contiguous or nullptr
+  const int32_t *seq_q;    // [B] or nullptr (= Tq)
+  const int32_t *seq_k;    // [B] or nullptr (= Tk)
+  int64_t sq_b, sq_t, sq_h;  // Q / O / dO / dQ
+  int64_t sk_b, sk_t, sk_h;  // K / V / dK / dV
+  int B, H, Tq, Tk;
+  int nblk;  // number of row blocks along the stationary sequence axis
+};
+
+__device__ __forceinline__ int clamp_len(const int32_t *lens, int b, int T) {
+  if (lens == nullptr) return T;
+  int L = lens[b];
+  return L < 0 ? 0 : (L > T ? T : L);
+}
+
+// sigmoid(s*scale + c) given x = s*(-scale*log2e) + (-c*log2e) (one FMA
+// before this call).  Hardware exp2 and reciprocal; x = +inf gives exactly 0.
+__device__ __forceinline__ float sigmoid_from_neg_log2(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x));
+}
+
+// Element-type traits: MFMA call and fp32 -> element conversions (RNE).
+template <typename T> struct Elem;
+
+template <> struct Elem<__bf16> {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t bits) {
+    return __builtin_bit_cast(float, (uint32_t)bits << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    return (uint16_t)(pack(x, 0.0f) & 0xffffu);
+  }
+};
+
+template <> struct Elem<_Float16> {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+};
+
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float to_f32(float x) { return x; }
+};
+
+// Round an fp32 value to the element type and back (P and dS are rounded to
+// the I/O dtype before their second product, as the reference kernels do).
+template <typename T> __device__ __forceinline__ float round_to(float x) {
+  return Elem<T>::to_f32(Elem<T>::from_f32(x));
+}
+template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
+
+// Gather element `e` (0..7) of four 16-byte rows into one 8-byte word
+// (row r in 16-bit lane r).
+__device__ __forceinline__ u32x2 gather4(const u32x4 &r0, const u32x4 &r1, const u32x4 &r2,
+                                         const u32x4 &r3, int e) {
+  const int w = e >> 1;
+  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+  u32x2 out;
+  out.x = __builtin_amdgcn_perm(r1[w], r0[w], sel);
+  out.y = __builtin_amdgcn_perm(r3[w], r2[w], sel);
+  return out;
+}
+
+// Same for two rows into one 4-byte word.
+__device__ __forceinline__ uint32_t gather2(const u32x4 &r0, const u32x4 &r1, int e) {
+  const int w = e >> 1;
+  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+  return __builtin_amdgcn_perm(r1[w], r0[w], sel);
+}
+
+__device__ __forceinline__ u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// Stages a ROWS x D tile of 16-bit elements (rows `row0 ..` of a [T, *, D]
+// tensor with row stride `stride`) through registers into LDS.  Each of the
+// 256 threads owns RPT consecutive rows x 8 columns, so the same registers can
+// be written row-major (pitch NP, 16-byte stores) and/or transposed
+// ([D][ROWS] with pitch TP, one 4- or 8-byte store per column).  Rows at or
+// past `nvalid` are zero-filled and never read from memory.
+template <int ROWS, int D> struct Stager {
+  static constexpr int RPT = ROWS * D / (8 * 256);
+  static constexpr int RG = ROWS / RPT;
+  static_assert(RPT == 2 || RPT == 4, "tile shape");
+  u32x4 r[RPT];
+
+  __device__ __forceinline__ void load(const uint16_t *base, int64_t stride, int row0, int nvalid,
+                                       int tid) {
+    const int rg = tid % RG, g = tid / RG;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int row = row0 + rg * RPT + i;
+      r[i] = row < nvalid ? *(const u32x4 *)(base + (int64_t)row * stride + 8 * g) : zero4();
+    }
+  }
+  template <int NP> __device__ __forceinline__ void store_nat(uint16_t *lds, int tid) const {
+    const int rg = tid % RG, g = tid / RG;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) *(u32x4 *)&lds[(rg * RPT + i) * NP + 8 * g] = r[i];
+  }
+  template <int TP> __device__ __forceinline__ void store_tr(uint16_t *lds, int tid) const {
+    const int rg = tid % RG, g = tid / RG;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t *dst = &lds[(8 * g + e) * TP + rg * RPT];
+      if constexpr (RPT == 4) *(u32x2 *)dst = gather4(r[0], r[1], r[2], r[3], e);
+      else *(uint32_t *)dst = gather2(r[0], r[1], e);
+    }
+  }
+};
+
+// A-operand read of a transposed tile ([D][rows] in LDS, pitch TP): row
+// `drow`, eight k-elements at rows 16*ks + 4h + {0..3} and 16*ks + 8 + 4h +
+// {0..3} — the key/query permutation of the C-layout-as-B-operand trick.
+template <int TP>
+__device__ __forceinline__ u32x4 read_tr_operand(const uint16_t *lds, int drow, int ks, int hi) {
+  const uint16_t *p = lds + drow * TP + 16 * ks + 4 * hi;
+  const u32x2 lo = *(const u32x2 *)p;
+  const u32x2 hv = *(const u32x2 *)(p + 8);
+  return (u32x4){lo.x, lo.y, hv.x, hv.y};
+}
+
+}  // namespace sigattn

@@ -1,0 +1,28 @@
+// Host-side launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace sigattn {
+
+// Element type codes (same values as enum sigattn_dtype in include/sigattn.h).
+constexpr int kF16 = 0;
+constexpr int kBF16 = 1;
+constexpr int kF32 = 2;
+
+// MFMA kernels: dtype in {kF16, kBF16}, D in {64, 128}, 16-byte aligned rows.
+void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
+                     hipStream_t st);
+void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
+                        hipStream_t st);
+void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
+                          hipStream_t st);
+
+// Portable kernels: any dtype, D in {16, 32, 64, 128}, any alignment.
+void launch_fwd_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
+void launch_bwd_dq_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
+void launch_bwd_dkdv_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
+
+}  // namespace sigattn

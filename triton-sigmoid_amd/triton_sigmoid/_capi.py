@@ -1,0 +1,201 @@
+"""ctypes binding of libsigattn.so (the C ABI in include/sigattn.h).
+
+The op bodies call `forward` / `backward` here.  They build one
+`sigattn_problem`, pass raw device pointers and torch's current HIP stream,
+and turn a non-zero status into RuntimeError.  There is no fallback: without
+the built library or a gfx950 device the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libsigattn.so"
+ABI_VERSION = 1
+
+F16, BF16, F32 = 0, 1, 2
+_DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+_c_i32, _c_i64, _c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+
+
+class SigattnProblem(ctypes.Structure):
+    """Mirror of `struct sigattn_problem` (include/sigattn.h)."""
+
+    _fields_ = [
+        ("abi_version", _c_i32),
+        ("dtype", _c_i32),
+        ("B", _c_i64),
+        ("Tq", _c_i64),
+        ("Tk", _c_i64),
+        ("H", _c_i64),
+        ("D", _c_i64),
+        ("q_stride_b", _c_i64),
+        ("q_stride_t", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("k_stride_b", _c_i64),
+        ("k_stride_t", _c_i64),
+        ("k_stride_h", _c_i64),
+        ("q", _c_vp),
+        ("k", _c_vp),
+        ("v", _c_vp),
+        ("bias", _c_vp),
+        ("scale", _c_vp),
+        ("score_mod", _c_vp),
+        ("seq_lens_q", _c_vp),
+        ("seq_lens_k", _c_vp),
+        ("causal", _c_i32),
+    ]
+
+
+# Exported symbols and their signatures (every function in include/sigattn.h).
+SIGNATURES = {
+    "sigattn_abi_version": ([], _c_i32),
+    "sigattn_strerror": ([_c_i32], ctypes.c_char_p),
+    "sigattn_check": ([ctypes.POINTER(SigattnProblem)], _c_i32),
+    "sigattn_fwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp], _c_i32),
+    "sigattn_bwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
+    "sigattn_bwd_dq": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp], _c_i32),
+    "sigattn_bwd_dkdv": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+_checked_devices: set[int] = set()
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Loads (once) and returns the C ABI library; raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise RuntimeError(
+                f"{p.name} is not built ({p}); build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` at the repository root"
+            )
+        lib = ctypes.CDLL(str(p))
+        for name, (argtypes, restype) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        if lib.sigattn_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{p.name} ABI version {lib.sigattn_abi_version()} != expected {ABI_VERSION}"
+            )
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def strerror(code: int) -> str:
+    return load_library().sigattn_strerror(code).decode()
+
+
+def _check_device(t: torch.Tensor) -> None:
+    if t.device.type != "cuda" or torch.version.hip is None:
+        raise RuntimeError(
+            "sigmoid attention kernels need tensors on an AMD gfx950 (MI355X) GPU under "
+            f"PyTorch-ROCm; got a tensor on '{t.device}'"
+        )
+    idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    if idx in _checked_devices:
+        return
+    arch = torch.cuda.get_device_properties(idx).gcnArchName.split(":")[0]
+    if arch != "gfx950":
+        raise RuntimeError(f"sigmoid attention kernels are built for gfx950 only; device {idx} is {arch}")
+    _checked_devices.add(idx)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) -> SigattnProblem:
+    B, Tq, H, D = Q.shape
+    Tk = K.shape[1]
+    qs, ks = Q.stride(), K.stride()
+    pr = SigattnProblem()
+    pr.abi_version = ABI_VERSION
+    pr.dtype = _DTYPE_CODE[Q.dtype]
+    pr.B, pr.Tq, pr.Tk, pr.H, pr.D = B, Tq, Tk, H, D
+    pr.q_stride_b, pr.q_stride_t, pr.q_stride_h = qs[0], qs[1], qs[2]
+    pr.k_stride_b, pr.k_stride_t, pr.k_stride_h = ks[0], ks[1], ks[2]
+    pr.q, pr.k, pr.v = _ptr(Q), _ptr(K), _ptr(V)
+    pr.bias, pr.scale = _ptr(bias), _ptr(sm_scale)
+    pr.score_mod = _ptr(score_mod)
+    pr.seq_lens_q, pr.seq_lens_k = _ptr(seq_lens_q), _ptr(seq_lens_k)
+    pr.causal = 1 if causal else 0
+    return pr
+
+
+def _prepare(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k):
+    """Canonicalises op inputs: contiguous rows, fp32 bias/scale/score_mod,
+    int32 seq_lens, everything on Q's device."""
+    if Q.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"unsupported dtype {Q.dtype}; expected float16, bfloat16 or float32")
+    if K.dtype != Q.dtype or V.dtype != Q.dtype:
+        raise RuntimeError(f"Q, K, V must share a dtype, got {Q.dtype}, {K.dtype}, {V.dtype}")
+    _check_device(Q)
+    dev = Q.device
+    Q, K, V = Q.contiguous(), K.contiguous(), V.contiguous()
+    for name, t in (("K", K), ("V", V)):
+        if t.device != dev:
+            raise RuntimeError(f"{name} is on {t.device}, expected {dev}")
+    bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+    sm_scale = sm_scale.to(device=dev, dtype=torch.float32).reshape(()).contiguous()
+    if score_mod is not None:
+        score_mod = score_mod.to(device=dev, dtype=torch.float32).contiguous()
+    if seq_lens_q is not None:
+        seq_lens_q = seq_lens_q.to(device=dev, dtype=torch.int32).contiguous()
+    if seq_lens_k is not None:
+        seq_lens_k = seq_lens_k.to(device=dev, dtype=torch.int32).contiguous()
+    return Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k
+
+
+def _raise(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {strerror(rc)} (status {rc})")
+
+
+def forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) -> torch.Tensor:
+    """O = sigmoid(QKᵀ·scale + bias + score_mod)·V via sigattn_fwd."""
+    lib = load_library()
+    Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k = _prepare(
+        Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
+    out = torch.empty_like(Q)
+    if out.numel() == 0:
+        return out
+    pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream(Q.device).cuda_stream
+        _raise(lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream), "sigattn_fwd")
+    return out
+
+
+def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):
+    """(dQ, dK, dV) via sigattn_bwd (dQ kernel, then dK/dV kernel)."""
+    lib = load_library()
+    Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k = _prepare(
+        Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
+    dO = dO.to(dtype=Q.dtype).contiguous()
+    if dO.shape != Q.shape:
+        raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
+    dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    if dQ.numel() == 0 and dK.numel() == 0:
+        return dQ, dK, dV
+    pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream(Q.device).cuda_stream
+        rc = lib.sigattn_bwd(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), stream)
+        _raise(rc, "sigattn_bwd")
+    return dQ, dK, dV
