@@ -17,20 +17,18 @@
 namespace sigattn {
 
 // ---------------------------------------------------------------------------
-// dQ: workgroup = 4 waves x 32 queries; walks 64-key tiles of K (row-major and
-// transposed) and V (row-major) staged in LDS.
+// dQ: workgroup = 4 waves x 32 queries; walks 64-key tiles of K and V staged
+// row-major in LDS (Kᵀ operands come from ds_read_b64_tr_b16).
 //   Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ (accumulators: lane = query column),
 //   dQᵀ += Kᵀ·dSᵀ with dSᵀ taken from the accumulator registers.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   constexpr int BM = 128, BN = 64;
-  constexpr int KP = D + 8, TP = BN + 4;
   constexpr int NKS = D / 16, NDB = D / 32;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sKt[D * TP];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[BN * D];  // swizzled tiles
+  __shared__ __attribute__((aligned(16))) uint16_t sV[BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? BN : 4];
 
   const int BH = p.B * p.H;
@@ -77,7 +75,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 #pragma unroll
   for (int d = 0; d < NDB; ++d) acc[d] = zero16();
 
-  Stager<BN, D> kst, vst;
+  TileStager<BN, D> kst, vst;
   float creg = 0.0f;
   auto gload = [&](int n0) {
     kst.load(Kb, p.sk_t, n0, Lk, tid);
@@ -92,9 +90,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   for (int it = 0; it < ntiles; ++it) {
     const int n0 = it * BN;
     __syncthreads();  // previous tile fully consumed
-    kst.template store_nat<KP>(sK, tid);
-    kst.template store_tr<TP>(sKt, tid);
-    vst.template store_nat<KP>(sV, tid);
+    kst.store(sK, tid);
+    vst.store(sV, tid);
     if (SCOREMOD && tid < BN) sC[tid] = creg;
     __syncthreads();
     if (it + 1 < ntiles) gload(n0 + BN);
@@ -110,12 +107,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
           continue;
         }
         f32x16 s = zero16(), dp = zero16();
-        const uint16_t *kr = &sK[(kb * 32 + l32) * KP + 8 * hi];
-        const uint16_t *vr = &sV[(kb * 32 + l32) * KP + 8 * hi];
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-          s = Elem<T>::mfma(*(const u32x4 *)(kr + 16 * ks), qf[ks], s);
-          dp = Elem<T>::mfma(*(const u32x4 *)(vr + 16 * ks), of[ks], dp);
+          s = Elem<T>::mfma(read_row_operand<D>(sK, kb * 32 + l32, ks, hi), qf[ks], s);
+          dp = Elem<T>::mfma(read_row_operand<D>(sV, kb * 32 + l32, ks, hi), of[ks], dp);
         }
         float c[16];
         if constexpr (SCOREMOD) {
@@ -152,7 +147,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
         const u32x4 bop = (u32x4){dsk[4 * ks], dsk[4 * ks + 1], dsk[4 * ks + 2], dsk[4 * ks + 3]};
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          acc[db] = Elem<T>::mfma(read_tr_operand<TP>(sKt, db * 32 + l32, ks, hi), bop, acc[db]);
+          acc[db] = Elem<T>::mfma(read_tr16_swz<D>(sK, db * 32, ks, lane), bop, acc[db]);
       }
     }
   }
@@ -175,21 +170,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO, each
-// staged row-major and transposed in LDS.
+// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO
+// staged row-major in LDS (Qᵀ, dOᵀ operands come from ds_read_b64_tr_b16).
 //   S = Q·Kᵀ, dP = dO·Vᵀ (accumulators: lane = key column),
 //   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS with P, dS taken from the accumulators.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
   constexpr int BN = 128, BMQ = 64;
-  constexpr int NP = D + 8, TP = BMQ + 4;
   constexpr int NKS = D / 16, NDB = D / 32;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[BMQ * NP];
-  __shared__ __attribute__((aligned(16))) uint16_t sO[BMQ * NP];
-  __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
-  __shared__ __attribute__((aligned(16))) uint16_t sOt[D * TP];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[BMQ * D];  // swizzled tiles
+  __shared__ __attribute__((aligned(16))) uint16_t sO[BMQ * D];
 
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -236,7 +228,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 #pragma unroll
   for (int d = 0; d < NDB; ++d) { dka[d] = zero16(); dva[d] = zero16(); }
 
-  Stager<BMQ, D> qst, ost;
+  TileStager<BMQ, D> qst, ost;
   if (ntiles > 0) {
     qst.load(Qb, p.sq_t, mstart, Lq, tid);
     ost.load(dOb, p.sq_t, mstart, Lq, tid);
@@ -244,10 +236,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   for (int it = 0; it < ntiles; ++it) {
     const int m0 = mstart + it * BMQ;
     __syncthreads();
-    qst.template store_nat<NP>(sQ, tid);
-    qst.template store_tr<TP>(sQt, tid);
-    ost.template store_nat<NP>(sO, tid);
-    ost.template store_tr<TP>(sOt, tid);
+    qst.store(sQ, tid);
+    ost.store(sO, tid);
     __syncthreads();
     if (it + 1 < ntiles) {
       qst.load(Qb, p.sq_t, m0 + BMQ, Lq, tid);
@@ -265,12 +255,10 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
           continue;
         }
         f32x16 s = zero16(), dp = zero16();
-        const uint16_t *qr = &sQ[(qbk * 32 + l32) * NP + 8 * hi];
-        const uint16_t *orr = &sO[(qbk * 32 + l32) * NP + 8 * hi];
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-          s = Elem<T>::mfma(*(const u32x4 *)(qr + 16 * ks), kf[ks], s);
-          dp = Elem<T>::mfma(*(const u32x4 *)(orr + 16 * ks), vf[ks], dp);
+          s = Elem<T>::mfma(read_row_operand<D>(sQ, qbk * 32 + l32, ks, hi), kf[ks], s);
+          dp = Elem<T>::mfma(read_row_operand<D>(sO, qbk * 32 + l32, ks, hi), vf[ks], dp);
         }
         float pv[16], ds[16];
 #pragma unroll
@@ -300,8 +288,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
         const u32x4 db_ = (u32x4){dsk[4 * ks], dsk[4 * ks + 1], dsk[4 * ks + 2], dsk[4 * ks + 3]};
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          dva[db] = Elem<T>::mfma(read_tr_operand<TP>(sOt, db * 32 + l32, ks, hi), pb, dva[db]);
-          dka[db] = Elem<T>::mfma(read_tr_operand<TP>(sQt, db * 32 + l32, ks, hi), db_, dka[db]);
+          dva[db] = Elem<T>::mfma(read_tr16_swz<D>(sO, db * 32, ks, lane), pb, dva[db]);
+          dka[db] = Elem<T>::mfma(read_tr16_swz<D>(sQ, db * 32, ks, lane), db_, dka[db]);
         }
       }
     }

@@ -133,6 +133,80 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// ---------------------------------------------------------------------------
+// Swizzled LDS tiles.  A [rows][D] tile of 16-bit elements is stored without
+// padding; its 16-byte chunk c of row r lives at chunk position c ^ swz(r).
+// With swz(r) = 4*(r&3) + ((r>>2)&3) (D = 128, 16 chunks per row) every access
+// pattern the kernels use is bank-conflict free on gfx950 (measured with
+// SQ_LDS_BANK_CONFLICT): 16-byte operand reads of 32 consecutive rows, the
+// 4-row x 32-column ds_read_b64_tr_b16 groups, and chunk-major 16-byte stores.
+// D = 64 (8 chunks per row, two rows per 64-bank line) uses
+// swz(r) = 4*((r>>1)&1) + ((r>>2)&3).
+template <int D> __device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
+  else return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+}
+// Element offset of (row, col) in a swizzled tile.
+template <int D> __device__ __forceinline__ int toff(int row, int col) {
+  return row * D + ((((col >> 3) ^ swz<D>(row)) << 3) | (col & 7));
+}
+
+// Stages a ROWS x D tile (rows `row0 ..` of a tensor with row stride
+// `stride`, elements) into a swizzled LDS tile through registers.  Thread t
+// owns chunks t, t+256, ... in row-major chunk order, so a wave loads whole
+// rows (coalesced) and stores them conflict-free.  Rows at or past `nvalid`
+// are zero-filled and never read from memory.
+template <int ROWS, int D> struct TileStager {
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int RPT = ROWS * CPR / 256;      // chunks per thread
+  static_assert(RPT >= 1 && ROWS * CPR % 256 == 0, "tile shape");
+  u32x4 r[RPT];
+
+  __device__ __forceinline__ void load(const uint16_t *base, int64_t stride, int row0, int nvalid,
+                                       int tid) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, ch = c % CPR;
+      r[i] = (row0 + row) < nvalid
+                 ? *(const u32x4 *)(base + (int64_t)(row0 + row) * stride + 8 * ch)
+                 : zero4();
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t *lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, ch = c % CPR;
+      *(u32x4 *)&lds[toff<D>(row, 8 * ch)] = r[i];
+    }
+  }
+};
+
+// 16-byte MFMA operand read from a swizzled tile: row `row`, k-elements
+// 16*ks + 8*hi .. +7 (k = 8h + j mapping).
+template <int D>
+__device__ __forceinline__ u32x4 read_row_operand(const uint16_t *lds, int row, int ks, int hi) {
+  return *(const u32x4 *)&lds[toff<D>(row, 16 * ks + 8 * hi)];
+}
+
+// Transposed MFMA operand read from a swizzled tile X[k][n] (see
+// read_tr16_operand for the lane mapping).
+template <int D>
+__device__ __forceinline__ u32x4 read_tr16_swz(const uint16_t *lds, int n0, int ks, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int grp = lane >> 4, s = lane & 15;
+  const int row = 16 * ks + 4 * (grp >> 1) + (s >> 2);
+  const int col = n0 + 16 * (grp & 1) + 4 * (s & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(lds + toff<D>(row, col)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(lds + toff<D>(row + 8, col)));
+  const u32x2 lo = __builtin_bit_cast(u32x2, a);
+  const u32x2 hv = __builtin_bit_cast(u32x2, b);
+  return (u32x4){lo.x, lo.y, hv.x, hv.y};
+}
+
 // Stages a ROWS x D tile of 16-bit elements (rows `row0 ..` of a [T, *, D]
 // tensor with row stride `stride`) through registers into LDS.  Each of the
 // 256 threads owns RPT consecutive rows x 8 columns, so the same registers can
@@ -169,6 +243,34 @@ template <int ROWS, int D> struct Stager {
     }
   }
 };
+
+// MFMA operand read of a row-major LDS tile X[k][n] (pitch NP elements) for
+// an operand that needs k along the eight elements of a lane and n = column
+// (n0 + l % 32), with the key/query permutation of the C-layout-as-B-operand
+// trick: element j of lane l is k = 16*ks + 4h + j (j < 4) or
+// 16*ks + 8 + 4h + (j - 4) (j >= 4), h = l / 32.
+//
+// ds_read_b64_tr_b16 (gfx950): inside each group of 16 lanes, the four
+// 16-bit elements read by source lane s form row s of a 16x4 matrix M, and
+// lane i receives M[4e + i/4][i%4] as element e.  Source lane s = 4e + m of a
+// group therefore supplies &X[k(e)][n_group + 4m]; lane i then holds column
+// n_group + i for the four k(e).  Two such reads give the eight elements.
+template <int NP>
+__device__ __forceinline__ u32x4 read_tr16_operand(const uint16_t *lds, int n0, int ks, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int grp = lane >> 4, s = lane & 15;
+  const int h = grp >> 1;
+  const int row = 16 * ks + 4 * h + (s >> 2);
+  const int col = n0 + 16 * (grp & 1) + 4 * (s & 3);
+  const uint16_t *p = lds + row * NP + col;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(p));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(p + 8 * NP));
+  const u32x2 lo = __builtin_bit_cast(u32x2, a);
+  const u32x2 hv = __builtin_bit_cast(u32x2, b);
+  return (u32x4){lo.x, lo.y, hv.x, hv.y};
+}
 
 // A-operand read of a transposed tile ([D][rows] in LDS, pitch TP): row
 // `drow`, eight k-elements at rows 16*ks + 4h + {0..3} and 16*ks + 8 + 4h +

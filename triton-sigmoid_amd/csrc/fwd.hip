@@ -10,11 +10,11 @@
 //
 // Structure (one workgroup = 4 waves = 128 queries of one (batch, head)):
 //   * each wave keeps its 32 query rows as MFMA operands in VGPRs;
-//   * 64-key tiles of K (row-major) and Vᵀ (transposed while staging) are
-//     double-buffered in LDS; the next tile's global loads are issued before
-//     the current tile's MFMAs;
+//   * 64-key tiles of K and V are double-buffered row-major in LDS; the next
+//     tile's global loads are issued before the current tile's MFMAs;
 //   * Sᵀ = K·Qᵀ (32x32x16 MFMA), sigmoid on the fp32 accumulators, then
-//     Oᵀ += Vᵀ·Pᵀ with Pᵀ taken straight from the Sᵀ accumulator registers;
+//     Oᵀ += Vᵀ·Pᵀ with Pᵀ taken straight from the Sᵀ accumulator registers and
+//     Vᵀ read from the row-major V tile with ds_read_b64_tr_b16;
 //   * causal: key tiles past the block's last query are never loaded, a wave
 //     skips 32-key blocks entirely above its rows, the element mask runs only
 //     on blocks that straddle the diagonal; the grid runs heaviest blocks first.
@@ -29,13 +29,12 @@ template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(const KParams p) {
   constexpr int BM = 128;      // queries per workgroup
   constexpr int BN = 64;       // keys per tile
-  constexpr int KP = D + 8;    // K row pitch in LDS (elements)
-  constexpr int VP = BN + 4;   // Vᵀ row pitch in LDS (elements)
   constexpr int NKS = D / 16;  // MFMA k-steps over the head dim
   constexpr int NDB = D / 32;  // 32-row blocks of Oᵀ
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][D * VP];
+  // Swizzled (unpadded) K and V tiles, two stages each.
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? 2 * BN : 4];
 
   const int BH = p.B * p.H;
@@ -82,7 +81,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(const KParams p) {
 #pragma unroll
   for (int d = 0; d < NDB; ++d) acc[d] = zero16();
 
-  Stager<BN, D> kst, vst;
+  TileStager<BN, D> kst, vst;
   float creg = 0.0f;
   auto gload = [&](int n0) {
     kst.load(Kb, p.sk_t, n0, Lk, tid);
@@ -93,8 +92,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(const KParams p) {
     }
   };
   auto lstore = [&](int st) {
-    kst.template store_nat<KP>(sK[st], tid);
-    vst.template store_tr<VP>(sV[st], tid);
+    kst.store(sK[st], tid);
+    vst.store(sV[st], tid);
     if (SCOREMOD && tid < BN) sC[st * BN + tid] = creg;
   };
 
@@ -121,9 +120,9 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(const KParams p) {
           continue;
         }
         f32x16 s = zero16();
-        const uint16_t *arow = &sK[st][(kb * 32 + l32) * KP + 8 * hi];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s = Elem<T>::mfma(*(const u32x4 *)(arow + 16 * ks), qf[ks], s);
+        for (int ks = 0; ks < NKS; ++ks)
+          s = Elem<T>::mfma(read_row_operand<D>(sK[st], kb * 32 + l32, ks, hi), qf[ks], s);
 
         float c[16];
         if constexpr (SCOREMOD) {
@@ -157,7 +156,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(const KParams p) {
         const u32x4 bop = (u32x4){pk[4 * ks], pk[4 * ks + 1], pk[4 * ks + 2], pk[4 * ks + 3]};
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          acc[db] = Elem<T>::mfma(read_tr_operand<VP>(sV[st], db * 32 + l32, ks, hi), bop, acc[db]);
+          acc[db] = Elem<T>::mfma(read_tr16_swz<D>(sV[st], db * 32, ks, lane), bop, acc[db]);
       }
     }
 
