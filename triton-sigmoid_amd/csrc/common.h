@@ -29,6 +29,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Kernel-local lambdas capture register arrays by reference; they must be
+// inlined or the arrays are demoted to scratch memory.
+#define SIGATTN_INLINE __attribute__((always_inline))
+
 // log2(e): sigmoid(x) = 1 / (1 + 2^(-x * log2(e))).
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -182,6 +186,95 @@ template <int ROWS, int D> struct TileStager {
     }
   }
 };
+
+// Loads rows [row0, row0 + ROWS) of a [*, D] tensor (row stride `stride`
+// elements) into the swizzled LDS tile `lds` with direct global->LDS DMA
+// (global_load_lds_dwordx4: lane i of a wave writes LDS bytes base + 16 i), so
+// no VGPRs hold the tile in flight.  Each wave-instruction fills 1 KB = 512/D
+// whole rows; lane i lands on physical chunk i % (D/8) of its row and
+// therefore fetches logical chunk (i % (D/8)) ^ swz(row).  Rows at or past
+// `nvalid` fetch row nvalid-1 instead (in bounds, finite); callers mask them.
+// Requires nvalid >= 1.  Completion is tracked by vmcnt: wait_dma() and a
+// barrier must precede reads of the tile.
+// The per-lane part (tile row and swizzled chunk byte offset of each of this
+// wave's instructions) is computed once; a tile load then costs one min and
+// one multiply-add per instruction, with a uniform (SGPR) base pointer and a
+// 32-bit byte offset (callers guarantee rows * stride * 2 < 2^31).
+template <int ROWS, int D, int NWAVES> struct DmaPlan {
+  static constexpr int CPR = D / 8;           // chunks per row
+  static constexpr int RPI = 64 / CPR;        // rows per wave-instruction
+  static constexpr int NI = ROWS / RPI / NWAVES;  // instructions per wave per tile
+  static_assert(ROWS % (RPI * NWAVES) == 0, "tile shape");
+  int row[NI];       // tile-relative row of this lane's chunk
+  int cbyte[NI];     // byte offset of the swizzled source chunk within its row
+  int r0[NI];        // first tile row of each instruction (wave-uniform)
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      r0[i] = (wave * NI + i) * RPI;
+      row[i] = r0[i] + lane / CPR;
+      cbyte[i] = 16 * ((lane % CPR) ^ swz<D>(row[i]));
+    }
+  }
+  // base: uniform pointer to row 0 of the (batch, head) slice.
+  __device__ __forceinline__ void issue(uint16_t *lds, const uint16_t *base, int stride_bytes,
+                                        int row0, int nvalid) const {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int g = min(row0 + row[i], nvalid - 1);
+      const uint32_t off = (uint32_t)g * (uint32_t)stride_bytes + (uint32_t)cbyte[i];
+      __builtin_amdgcn_global_load_lds((const char *)base + off,
+                                       (__attribute__((address_space(3))) void *)(lds + r0[i] * D),
+                                       16, 0, 0);
+    }
+  }
+};
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Per-lane element offsets into swizzled [*, D] tiles, computed once per
+// kernel.  A row offset that is a multiple of 16 rows leaves swz() unchanged,
+// so such offsets (tile stages, 16-row k-steps, 32-row blocks) are added as
+// compile-time constants and fold into the ds_read immediate.
+template <int D> struct TileOffsets {
+  int row_op[D / 16];   // 16-byte operand at row l%32, k-step ks (read_row_operand)
+  int tr_op[D / 32][2]; // tr16 reads for column block db, first / second 4-row group
+  __device__ __forceinline__ void init(int lane) {
+    const int l32 = lane & 31, hi = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) row_op[ks] = toff<D>(l32, 16 * ks + 8 * hi);
+    const int grp = lane >> 4, s = lane & 15;
+    const int row = 4 * (grp >> 1) + (s >> 2);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = db * 32 + 16 * (grp & 1) + 4 * (s & 3);
+      tr_op[db][0] = toff<D>(row, col);
+      tr_op[db][1] = toff<D>(row + 8, col);
+    }
+  }
+};
+
+// Operand read at row (row16 + l%32) where row16 is a multiple of 16.
+template <int D>
+__device__ __forceinline__ u32x4 ld_row(const uint16_t *lds, const TileOffsets<D> &o, int row16,
+                                        int ks) {
+  return *(const u32x4 *)&lds[row16 * D + o.row_op[ks]];
+}
+
+// Transposed operand (see read_tr16_operand) for k-step ks, column block db.
+template <int D>
+__device__ __forceinline__ u32x4 ld_tr(const uint16_t *lds, const TileOffsets<D> &o, int ks, int db) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const uint16_t *base = lds + 16 * ks * D;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(base + o.tr_op[db][0]));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(base + o.tr_op[db][1]));
+  const u32x2 lo = __builtin_bit_cast(u32x2, a);
+  const u32x2 hv = __builtin_bit_cast(u32x2, b);
+  return (u32x4){lo.x, lo.y, hv.x, hv.y};
+}
 
 // 16-byte MFMA operand read from a swizzled tile: row `row`, k-elements
 // 16*ks + 8*hi .. +7 (k = 8h + j mapping).
