@@ -9,27 +9,37 @@
 //   dP = dO·Vᵀ; dS = P(1-P)dP computed as fma(P, -P*dP, P*dP); masked dS = 0;
 //   dQ = (dS rounded to the I/O dtype)·K · scale;
 //   dV = (P rounded)ᵀ·dO;  dK = (dS rounded)ᵀ·Q · scale.
-// Padded query rows get dQ = 0 and padded key rows dK = dV = 0; zero-filled
-// rows past seq_lens contribute exactly 0, so only causal needs an element mask.
+// Padded query rows get dQ = 0 and padded key rows dK = dV = 0.
+//
+// Both kernels stream their tiles (K, V for dQ; Q, dO for dK/dV) into
+// double-buffered swizzled LDS with direct global->LDS DMA one tile ahead,
+// and keep the stationary rows as MFMA operands in registers.  The dK/dV
+// kernel (one wave per SIMD, accumulators in AGPRs) runs each tile as
+// scheduling regions that overlap the P / dS VALU work of one 32-query block
+// with the MFMA chains of the next; the dQ kernel (two waves per SIMD) relies
+// on the second wave for that overlap.  Rows past seq_lens are fetched as
+// copies of the last valid row (in bounds) and masked on boundary tiles.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
 namespace sigattn {
 
 // ---------------------------------------------------------------------------
-// dQ: workgroup = 4 waves x 32 queries; walks 64-key tiles of K and V staged
-// row-major in LDS (Kᵀ operands come from ds_read_b64_tr_b16).
+// dQ: workgroup = 4 waves x 32 queries; walks 64-key tiles of K and V.
 //   Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ (accumulators: lane = query column),
-//   dQᵀ += Kᵀ·dSᵀ with dSᵀ taken from the accumulator registers.
+//   dQᵀ += Kᵀ·dSᵀ with dSᵀ taken from the accumulator registers and Kᵀ read
+//   from the K tile with ds_read_b64_tr_b16.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int NKS = D / 16, NDB = D / 32;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[BN * D];  // swizzled tiles
-  __shared__ __attribute__((aligned(16))) uint16_t sV[BN * D];
-  __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? BN : 4];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * D];
+  __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? 2 * BN : 4];
 
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -75,81 +85,107 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 #pragma unroll
   for (int d = 0; d < NDB; ++d) acc[d] = zero16();
 
-  TileStager<BN, D> kst, vst;
+  TileOffsets<D> to;
+  to.init(lane);
+  DmaPlan<BN, D, 4> dma;
+  dma.init(w, lane);
+  const int kv_stride_bytes = (int)(p.sk_t * 2);
+
+  // dS of one 32-key block into eight packed words.
+  auto ds_block = [&](const f32x16 &s, const f32x16 &dp, int st, int kl, int kbase, uint32_t *out,
+                      bool mask) SIGATTN_INLINE {
+    float c[16];
+    if constexpr (SCOREMOD) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 cv = *(const float4 *)&sC[st * BN + kl + 8 * g + 4 * hi];
+        c[4 * g + 0] = cv.x; c[4 * g + 1] = cv.y; c[4 * g + 2] = cv.z; c[4 * g + 3] = cv.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) c[i] = nbl;
+    }
+    float ds[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float pr = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, c[i]));
+      const float t = pr * dp[i];
+      ds[i] = __builtin_fmaf(-pr, t, t);
+    }
+    if (mask) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kbase + 8 * (i / 4) + 4 * hi + (i % 4);
+        if (key >= Lk || (CAUSAL && key > my_q)) ds[i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = Elem<T>::pack(ds[2 * i], ds[2 * i + 1]);
+  };
+
+  // dQᵀ[d, q] += Kᵀ[d, key] · dSᵀ[key, q] for the two 16-key steps of block kbi.
+  auto dq_block = [&](int st, int kbi, const uint32_t *dsk) SIGATTN_INLINE {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 bop = (u32x4){dsk[4 * j], dsk[4 * j + 1], dsk[4 * j + 2], dsk[4 * j + 3]};
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        acc[db] = Elem<T>::mfma(ld_tr<D>(sK[st], to, 2 * kbi + j, db), bop, acc[db]);
+    }
+  };
+
+  // Per 32-key block: Sᵀ/dPᵀ chains (16 MFMA), dS (VALU), dQ (8 MFMA).  The
+  // blocks run one after the other (four 32x32 fp32 accumulators plus the Q
+  // and dO operands would not fit next to the dQ accumulators); the second
+  // wave on each SIMD supplies the MFMA/VALU overlap.
+  auto tile_step = [&](int st, int n0, bool mask) SIGATTN_INLINE {
+#pragma unroll
+    for (int kbi = 0; kbi < 2; ++kbi) {
+      f32x16 s = zero16(), dp = zero16();
+      uint32_t dk[8];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        s = Elem<T>::mfma(ld_row<D>(sK[st], to, 32 * kbi, ks), qf[ks], s);
+        dp = Elem<T>::mfma(ld_row<D>(sV[st], to, 32 * kbi, ks), of[ks], dp);
+      }
+      ds_block(s, dp, st, 32 * kbi, n0 + 32 * kbi, dk, mask);
+      dq_block(st, kbi, dk);
+    }
+  };
+
   float creg = 0.0f;
-  auto gload = [&](int n0) {
-    kst.load(Kb, p.sk_t, n0, Lk, tid);
-    vst.load(Vb, p.sk_t, n0, Lk, tid);
+  auto load_c = [&](int n0) SIGATTN_INLINE {
     if (SCOREMOD && tid < BN) {
       const int key = n0 + tid;
       creg = key < Lk ? -(bias + p.score_mod[(int64_t)b * p.Tk + key]) * kLog2e : 0.0f;
     }
   };
-
-  if (ntiles > 0) gload(0);
-  for (int it = 0; it < ntiles; ++it) {
+  auto issue = [&](int st, int n0) SIGATTN_INLINE {
+    dma.issue(sK[st], Kb, kv_stride_bytes, n0, Lk);
+    dma.issue(sV[st], Vb, kv_stride_bytes, n0, Lk);
+  };
+  auto iteration = [&](int it, auto stage_tag) SIGATTN_INLINE {
+    constexpr int ST = decltype(stage_tag)::value;
     const int n0 = it * BN;
-    __syncthreads();  // previous tile fully consumed
-    kst.store(sK, tid);
-    vst.store(sV, tid);
-    if (SCOREMOD && tid < BN) sC[tid] = creg;
+    wait_dma();
+    if (SCOREMOD && tid < BN) sC[ST * BN + tid] = creg;
     __syncthreads();
-    if (it + 1 < ntiles) gload(n0 + BN);
-
-    if (!CAUSAL || n0 <= qw + 31) {
-      uint32_t dsk[BN / 4];
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb) {
-        const int kbase = n0 + kb * 32;
-        if (CAUSAL && kbase > qw + 31) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) dsk[kb * 8 + i] = 0u;
-          continue;
-        }
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          s = Elem<T>::mfma(read_row_operand<D>(sK, kb * 32 + l32, ks, hi), qf[ks], s);
-          dp = Elem<T>::mfma(read_row_operand<D>(sV, kb * 32 + l32, ks, hi), of[ks], dp);
-        }
-        float c[16];
-        if constexpr (SCOREMOD) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 cv = *(const float4 *)&sC[kb * 32 + 8 * g + 4 * hi];
-            c[4 * g + 0] = cv.x; c[4 * g + 1] = cv.y; c[4 * g + 2] = cv.z; c[4 * g + 3] = cv.w;
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) c[i] = nbl;
-        }
-        float ds[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float pr = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, c[i]));
-          const float t = pr * dp[i];
-          ds[i] = __builtin_fmaf(-pr, t, t);
-        }
-        if (CAUSAL && kbase + 31 > qw) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kbase + 8 * (i / 4) + 4 * hi + (i % 4);
-            if (key > my_q) ds[i] = 0.0f;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dsk[kb * 8 + i] = Elem<T>::pack(ds[2 * i], ds[2 * i + 1]);
-      }
-      // dQᵀ[d, q] += Kᵀ[d, key] · dSᵀ[key, q]
-#pragma unroll
-      for (int ks = 0; ks < BN / 16; ++ks) {
-        if (CAUSAL && n0 + ks * 16 > qw + 31) break;
-        const u32x4 bop = (u32x4){dsk[4 * ks], dsk[4 * ks + 1], dsk[4 * ks + 2], dsk[4 * ks + 3]};
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          acc[db] = Elem<T>::mfma(read_tr16_swz<D>(sK, db * 32, ks, lane), bop, acc[db]);
-      }
+    if (it + 1 < ntiles) {
+      load_c(n0 + BN);
+      issue(ST ^ 1, n0 + BN);
     }
+    if (!CAUSAL || n0 <= qw + 31) {
+      tile_step(ST, n0, (n0 + BN > Lk) || (CAUSAL && n0 + BN - 1 > qw));
+    }
+  };
+
+  if (ntiles > 0) {
+    load_c(0);
+    issue(0, 0);
+  }
+  for (int it = 0; it < ntiles; it += 2) {
+    iteration(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) iteration(it + 1, std::integral_constant<int, 1>{});
   }
 
   if (my_q < p.Tq) {
@@ -161,8 +197,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
       for (int g = 0; g < 4; ++g) {
         const int d0 = db * 32 + 8 * g + 4 * hi;
         u32x2 o;
-        o.x = valid ? Elem<T>::pack(acc[db][4 * g] * scale, acc[db][4 * g + 1] * scale) : 0u;
-        o.y = valid ? Elem<T>::pack(acc[db][4 * g + 2] * scale, acc[db][4 * g + 3] * scale) : 0u;
+        o.x = Elem<T>::pack(acc[db][4 * g] * scale, acc[db][4 * g + 1] * scale);
+        o.y = Elem<T>::pack(acc[db][4 * g + 2] * scale, acc[db][4 * g + 3] * scale);
+        if (!valid) o = (u32x2){0u, 0u};
         *(u32x2 *)(row + d0) = o;
       }
     }
@@ -170,18 +207,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO
-// staged row-major in LDS (Qᵀ, dOᵀ operands come from ds_read_b64_tr_b16).
+// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO.
 //   S = Q·Kᵀ, dP = dO·Vᵀ (accumulators: lane = key column),
-//   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS with P, dS taken from the accumulators.
+//   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS with P, dS taken from the accumulators and
+//   Qᵀ, dOᵀ read from the tiles with ds_read_b64_tr_b16.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
   constexpr int BN = 128, BMQ = 64;
   constexpr int NKS = D / 16, NDB = D / 32;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[BMQ * D];  // swizzled tiles
-  __shared__ __attribute__((aligned(16))) uint16_t sO[BMQ * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BMQ * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sO[2][BMQ * D];
 
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -228,71 +265,114 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 #pragma unroll
   for (int d = 0; d < NDB; ++d) { dka[d] = zero16(); dva[d] = zero16(); }
 
-  TileStager<BMQ, D> qst, ost;
-  if (ntiles > 0) {
-    qst.load(Qb, p.sq_t, mstart, Lq, tid);
-    ost.load(dOb, p.sq_t, mstart, Lq, tid);
-  }
-  for (int it = 0; it < ntiles; ++it) {
-    const int m0 = mstart + it * BMQ;
-    __syncthreads();
-    qst.store(sQ, tid);
-    ost.store(sO, tid);
-    __syncthreads();
-    if (it + 1 < ntiles) {
-      qst.load(Qb, p.sq_t, m0 + BMQ, Lq, tid);
-      ost.load(dOb, p.sq_t, m0 + BMQ, Lq, tid);
-    }
+  TileOffsets<D> to;
+  to.init(lane);
+  DmaPlan<BMQ, D, 4> dma;
+  dma.init(w, lane);
+  const int q_stride_bytes = (int)(p.sq_t * 2);
 
-    if (!CAUSAL || m0 + BMQ - 1 >= kw) {
-      uint32_t pk[BMQ / 4], dsk[BMQ / 4];
+  // P and dS of one 32-query block (rows qbase.., this lane's key).
+  auto pds_block = [&](const f32x16 &s, const f32x16 &dp, int qbase, uint32_t *pk, uint32_t *dsk,
+                       bool mask) SIGATTN_INLINE {
+    float pv[16], ds[16];
 #pragma unroll
-      for (int qbk = 0; qbk < BMQ / 32; ++qbk) {
-        const int qbase = m0 + qbk * 32;
-        if (CAUSAL && qbase + 31 < kw) {
+    for (int i = 0; i < 16; ++i) {
+      pv[i] = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, nc));
+      const float t = pv[i] * dp[i];
+      ds[i] = __builtin_fmaf(-pv[i], t, t);
+    }
+    if (mask) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) { pk[qbk * 8 + i] = 0u; dsk[qbk * 8 + i] = 0u; }
-          continue;
-        }
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          s = Elem<T>::mfma(read_row_operand<D>(sQ, qbk * 32 + l32, ks, hi), kf[ks], s);
-          dp = Elem<T>::mfma(read_row_operand<D>(sO, qbk * 32 + l32, ks, hi), vf[ks], dp);
-        }
-        float pv[16], ds[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          pv[i] = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, nc));
-          const float t = pv[i] * dp[i];
-          ds[i] = __builtin_fmaf(-pv[i], t, t);
-        }
-        if (CAUSAL && qbase < kw + 31) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int q = qbase + 8 * (i / 4) + 4 * hi + (i % 4);
-            if (q < my_k) { pv[i] = 0.0f; ds[i] = 0.0f; }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pk[qbk * 8 + i] = Elem<T>::pack(pv[2 * i], pv[2 * i + 1]);
-          dsk[qbk * 8 + i] = Elem<T>::pack(ds[2 * i], ds[2 * i + 1]);
-        }
-      }
-      // dVᵀ[d, key] += dOᵀ[d, q] · P[q, key];  dKᵀ[d, key] += Qᵀ[d, q] · dS[q, key]
-#pragma unroll
-      for (int ks = 0; ks < BMQ / 16; ++ks) {
-        if (CAUSAL && m0 + ks * 16 + 15 < kw) continue;
-        const u32x4 pb = (u32x4){pk[4 * ks], pk[4 * ks + 1], pk[4 * ks + 2], pk[4 * ks + 3]};
-        const u32x4 db_ = (u32x4){dsk[4 * ks], dsk[4 * ks + 1], dsk[4 * ks + 2], dsk[4 * ks + 3]};
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          dva[db] = Elem<T>::mfma(read_tr16_swz<D>(sO, db * 32, ks, lane), pb, dva[db]);
-          dka[db] = Elem<T>::mfma(read_tr16_swz<D>(sQ, db * 32, ks, lane), db_, dka[db]);
-        }
+      for (int i = 0; i < 16; ++i) {
+        const int q = qbase + 8 * (i / 4) + 4 * hi + (i % 4);
+        if (q >= Lq || (CAUSAL && q < my_k)) { pv[i] = 0.0f; ds[i] = 0.0f; }
       }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pk[i] = Elem<T>::pack(pv[2 * i], pv[2 * i + 1]);
+      dsk[i] = Elem<T>::pack(ds[2 * i], ds[2 * i + 1]);
+    }
+  };
+
+  // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS for the two 16-query steps of block qbk.
+  auto grad_block = [&](int st, int qbk, const uint32_t *pk, const uint32_t *dsk) SIGATTN_INLINE {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 pb = (u32x4){pk[4 * j], pk[4 * j + 1], pk[4 * j + 2], pk[4 * j + 3]};
+      const u32x4 sb = (u32x4){dsk[4 * j], dsk[4 * j + 1], dsk[4 * j + 2], dsk[4 * j + 3]};
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        dva[db] = Elem<T>::mfma(ld_tr<D>(sO[st], to, 2 * qbk + j, db), pb, dva[db]);
+        dka[db] = Elem<T>::mfma(ld_tr<D>(sQ[st], to, 2 * qbk + j, db), sb, dka[db]);
+      }
+    }
+  };
+
+  // Regions: A S0/dP0 chains; B S1/dP1 chains || P,dS of block 0;
+  // C grads of block 0 || P,dS of block 1; D grads of block 1.
+  auto tile_step = [&](int st, int m0, bool mask) SIGATTN_INLINE {
+    f32x16 s0 = zero16(), d0 = zero16(), s1 = zero16(), d1 = zero16();
+    uint32_t p0[8], g0[8], p1[8], g1[8];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      s0 = Elem<T>::mfma(ld_row<D>(sQ[st], to, 0, ks), kf[ks], s0);
+      d0 = Elem<T>::mfma(ld_row<D>(sO[st], to, 0, ks), vf[ks], d0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      s1 = Elem<T>::mfma(ld_row<D>(sQ[st], to, 32, ks), kf[ks], s1);
+      d1 = Elem<T>::mfma(ld_row<D>(sO[st], to, 32, ks), vf[ks], d1);
+    }
+    pds_block(s0, d0, m0, p0, g0, mask);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * NKS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    grad_block(st, 0, p0, g0);
+    pds_block(s1, d1, m0 + 32, p1, g1, mask);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 4 * NDB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    grad_block(st, 1, p1, g1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 4 * NDB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  auto issue = [&](int st, int m0) SIGATTN_INLINE {
+    dma.issue(sQ[st], Qb, q_stride_bytes, m0, Lq);
+    dma.issue(sO[st], dOb, q_stride_bytes, m0, Lq);
+  };
+  auto iteration = [&](int it, auto stage_tag) SIGATTN_INLINE {
+    constexpr int ST = decltype(stage_tag)::value;
+    const int m0 = mstart + it * BMQ;
+    wait_dma();
+    __syncthreads();
+    if (it + 1 < ntiles) issue(ST ^ 1, m0 + BMQ);
+    if (!CAUSAL || m0 + BMQ - 1 >= kw) {
+      tile_step(ST, m0, (m0 + BMQ > Lq) || (CAUSAL && m0 < kw + 31));
+    }
+  };
+
+  if (ntiles > 0) issue(0, mstart);
+  for (int it = 0; it < ntiles; it += 2) {
+    iteration(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) iteration(it + 1, std::integral_constant<int, 1>{});
   }
 
   if (my_k < p.Tk) {
@@ -304,10 +384,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       for (int g = 0; g < 4; ++g) {
         const int d0 = db * 32 + 8 * g + 4 * hi;
         u32x2 ok_, ov;
-        ok_.x = kok ? Elem<T>::pack(dka[db][4 * g] * scale, dka[db][4 * g + 1] * scale) : 0u;
-        ok_.y = kok ? Elem<T>::pack(dka[db][4 * g + 2] * scale, dka[db][4 * g + 3] * scale) : 0u;
-        ov.x = kok ? Elem<T>::pack(dva[db][4 * g], dva[db][4 * g + 1]) : 0u;
-        ov.y = kok ? Elem<T>::pack(dva[db][4 * g + 2], dva[db][4 * g + 3]) : 0u;
+        ok_.x = Elem<T>::pack(dka[db][4 * g] * scale, dka[db][4 * g + 1] * scale);
+        ok_.y = Elem<T>::pack(dka[db][4 * g + 2] * scale, dka[db][4 * g + 3] * scale);
+        ov.x = Elem<T>::pack(dva[db][4 * g], dva[db][4 * g + 1]);
+        ov.y = Elem<T>::pack(dva[db][4 * g + 2], dva[db][4 * g + 3]);
+        if (!kok) { ok_ = (u32x2){0u, 0u}; ov = (u32x2){0u, 0u}; }
         *(u32x2 *)(kr + d0) = ok_;
         *(u32x2 *)(vr + d0) = ov;
       }
