@@ -141,6 +141,28 @@ def cpu_baseline(cfg, budget_s: float = 20.0):
     }
 
 
+def copy_calibration(nbytes: int = 1 << 30) -> None:
+    """Runs one plain device copy of `nbytes` (read nbytes + write nbytes) so
+    rocprofv3's FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes."""
+    import torch
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: {nbytes} bytes read, {nbytes} bytes written")
+
+
+def load_traffic(kernel: str, config: str):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc FETCH_SIZE
+    and WRITE_SIZE (scaled by the copy calibration), from profiles/hbm_traffic.json."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    entry = data.get(config, {}).get(kernel)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,7 +170,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -237,7 +264,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": load_traffic(dominant, args.config),
         },
         "cpu_baseline": cpu,
     }

@@ -1,0 +1,137 @@
+"""CPU tests of the C ABI (include/sigattn.h, libsigattn.so): symbols, struct
+layout, validation and error codes.  No kernel is launched: every call here
+returns before any HIP call."""
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from triton_sigmoid import _capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "sigattn.h"
+
+pytestmark = pytest.mark.skipif(not _capi.LIB_PATH.exists(), reason="libsigattn.so not built")
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sigattn_\w+)\s*\(", text)))
+
+
+def _problem(**kw):
+    p = _capi.SigattnProblem()
+    p.abi_version = _capi.ABI_VERSION
+    p.dtype = _capi.BF16
+    p.B, p.Tq, p.Tk, p.H, p.D = 2, 16, 16, 2, 64
+    p.q_stride_b, p.q_stride_t, p.q_stride_h = 16 * 2 * 64, 2 * 64, 64
+    p.k_stride_b, p.k_stride_t, p.k_stride_h = 16 * 2 * 64, 2 * 64, 64
+    fake = 1 << 20  # never dereferenced: validation fails or the problem is empty
+    p.q = p.k = p.v = fake
+    p.bias = p.scale = fake
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_capi.LIB_PATH))
+    declared = _declared_functions()
+    assert declared == sorted(_capi.SIGNATURES), declared
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_strerror():
+    lib = _capi.load_library()
+    assert lib.sigattn_abi_version() == _capi.ABI_VERSION
+    assert lib.sigattn_strerror(0) == b"success"
+    for code in range(-8, 0):
+        assert lib.sigattn_strerror(code) not in (b"", b"unknown sigattn status")
+    assert lib.sigattn_strerror(-99) == b"unknown sigattn status"
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_header(tmp_path):
+    fields = [f[0] for f in _capi.SigattnProblem._fields_]
+    src = tmp_path / "layout.c"
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(sigattn_problem, {f}));' for f in fields)
+    src.write_text(
+        "#include <stddef.h>\n#include <stdio.h>\n#include \"sigattn.h\"\n"
+        "int main(void) {\n" + body + '\n  printf("sizeof %zu\\n", sizeof(sigattn_problem));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for f in fields:
+        assert int(out[f]) == getattr(_capi.SigattnProblem, f).offset, f
+    assert int(out["sizeof"]) == ctypes.sizeof(_capi.SigattnProblem)
+
+
+@pytest.mark.parametrize("change,code", [
+    (dict(abi_version=99), -7),
+    (dict(dtype=7), -2),
+    (dict(D=48), -3),
+    (dict(D=256), -3),
+    (dict(B=-1), -4),
+    (dict(Tq=1 << 40), -4),
+    (dict(k_stride_t=-5), -5),
+    (dict(Tk=8), -6),           # dense (no seq_lens) requires Tq == Tk
+    (dict(bias=None), -1),
+    (dict(scale=None), -1),
+    (dict(q=None), -1),
+    (dict(v=None), -1),
+])
+def test_validation_error_codes(change, code):
+    lib = _capi.load_library()
+    p = _problem(**change)
+    assert lib.sigattn_check(ctypes.byref(p)) == code
+    assert lib.sigattn_fwd(ctypes.byref(p), 1 << 20, None) == code
+    assert lib.sigattn_bwd(ctypes.byref(p), 1 << 20, 1 << 20, 1 << 20, 1 << 20, None) == code
+
+
+def test_null_problem_and_null_outputs():
+    lib = _capi.load_library()
+    assert lib.sigattn_check(None) == -1
+    assert lib.sigattn_fwd(None, 1 << 20, None) == -1
+    p = _problem()
+    assert lib.sigattn_check(ctypes.byref(p)) == 0
+    assert lib.sigattn_fwd(ctypes.byref(p), None, None) == -1
+    assert lib.sigattn_bwd(ctypes.byref(p), 1 << 20, None, 1 << 20, 1 << 20, None) == -1
+    assert lib.sigattn_bwd(ctypes.byref(p), None, 1 << 20, 1 << 20, 1 << 20, None) == -1
+    assert lib.sigattn_bwd_dq(ctypes.byref(p), 1 << 20, None, None) == -1
+    assert lib.sigattn_bwd_dkdv(ctypes.byref(p), 1 << 20, 1 << 20, None, None) == -1
+
+
+def test_cross_attention_allowed_with_seq_lens():
+    lib = _capi.load_library()
+    p = _problem(Tk=8, seq_lens_k=1 << 20, seq_lens_q=1 << 20)
+    assert lib.sigattn_check(ctypes.byref(p)) == 0
+
+
+def test_empty_problems_return_before_any_launch():
+    lib = _capi.load_library()
+    for change in (dict(B=0), dict(H=0), dict(B=0, q=None, k=None, v=None, bias=None, scale=None)):
+        p = _problem(**change)
+        assert lib.sigattn_fwd(ctypes.byref(p), None, None) == 0
+        assert lib.sigattn_bwd(ctypes.byref(p), None, None, None, None, None) == 0
+    p = _problem(Tq=0, Tk=0)
+    assert lib.sigattn_fwd(ctypes.byref(p), None, None) == 0
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("src", ["fwd.hip", "bwd.hip", "generic.hip"])
+def test_device_code_has_no_packed_fp32_instructions(src):
+    """Every HIP source is built with packed-fp32 selection disabled; check the
+    gfx950 assembly of each kernel file."""
+    from triton_sigmoid import _build
+    cmd = [_build.hipcc(), *_build.compile_flags(), "-S", "--cuda-device-only",
+           str(_build.CSRC / src), "-o", "-"]
+    asm = subprocess.run(cmd, capture_output=True, text=True, check=True).stdout
+    assert "v_mfma" in asm or src == "generic.hip"
+    assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)
