@@ -207,14 +207,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO.
+// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO,
+// two 32-query blocks at a time.
 //   S = Q·Kᵀ, dP = dO·Vᵀ (accumulators: lane = key column),
 //   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS with P, dS taken from the accumulators and
 //   Qᵀ, dOᵀ read from the tiles with ds_read_b64_tr_b16.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
-  constexpr int BN = 128, BMQ = 64;
+  constexpr int BN = 128, BMQ = 64;  // keys per workgroup, queries per LDS tile
   constexpr int NKS = D / 16, NDB = D / 32;
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BMQ * D];
@@ -309,23 +310,24 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     }
   };
 
-  // Regions: A S0/dP0 chains; B S1/dP1 chains || P,dS of block 0;
+  // One pair of 32-query blocks (tile rows qo .. qo+63) in four regions:
+  // A S0/dP0 chains; B S1/dP1 chains || P,dS of block 0;
   // C grads of block 0 || P,dS of block 1; D grads of block 1.
-  auto tile_step = [&](int st, int m0, bool mask) SIGATTN_INLINE {
+  auto pair_step = [&](int st, int m0, int qo, bool mask) SIGATTN_INLINE {
     f32x16 s0 = zero16(), d0 = zero16(), s1 = zero16(), d1 = zero16();
     uint32_t p0[8], g0[8], p1[8], g1[8];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      s0 = Elem<T>::mfma(ld_row<D>(sQ[st], to, 0, ks), kf[ks], s0);
-      d0 = Elem<T>::mfma(ld_row<D>(sO[st], to, 0, ks), vf[ks], d0);
+      s0 = Elem<T>::mfma(ld_row<D>(sQ[st], to, qo, ks), kf[ks], s0);
+      d0 = Elem<T>::mfma(ld_row<D>(sO[st], to, qo, ks), vf[ks], d0);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      s1 = Elem<T>::mfma(ld_row<D>(sQ[st], to, 32, ks), kf[ks], s1);
-      d1 = Elem<T>::mfma(ld_row<D>(sO[st], to, 32, ks), vf[ks], d1);
+      s1 = Elem<T>::mfma(ld_row<D>(sQ[st], to, qo + 32, ks), kf[ks], s1);
+      d1 = Elem<T>::mfma(ld_row<D>(sO[st], to, qo + 32, ks), vf[ks], d1);
     }
-    pds_block(s0, d0, m0, p0, g0, mask);
+    pds_block(s0, d0, m0 + qo, p0, g0, mask);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 2 * NKS; ++i) {
@@ -334,8 +336,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    grad_block(st, 0, p0, g0);
-    pds_block(s1, d1, m0 + 32, p1, g1, mask);
+    grad_block(st, qo / 32, p0, g0);
+    pds_block(s1, d1, m0 + qo + 32, p1, g1, mask);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 4 * NDB; ++i) {
@@ -344,7 +346,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    grad_block(st, 1, p1, g1);
+    grad_block(st, qo / 32 + 1, p1, g1);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 4 * NDB; ++i) {
@@ -352,6 +354,16 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // A 128-query tile = two pairs; each pair masks / skips on its own rows.
+  auto tile_step = [&](int st, int m0) SIGATTN_INLINE {
+#pragma unroll
+    for (int qo = 0; qo < BMQ; qo += 64) {
+      const int mq = m0 + qo;
+      if (CAUSAL && mq + 63 < kw) continue;  // every query of the pair precedes this wave's keys
+      pair_step(st, m0, qo, (mq + 64 > Lq) || (CAUSAL && mq < kw + 31));
+    }
   };
 
   auto issue = [&](int st, int m0) SIGATTN_INLINE {
@@ -364,9 +376,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     wait_dma();
     __syncthreads();
     if (it + 1 < ntiles) issue(ST ^ 1, m0 + BMQ);
-    if (!CAUSAL || m0 + BMQ - 1 >= kw) {
-      tile_step(ST, m0, (m0 + BMQ > Lq) || (CAUSAL && m0 < kw + 31));
-    }
+    if (!CAUSAL || m0 + BMQ - 1 >= kw) tile_step(ST, m0);
   };
 
   if (ntiles > 0) issue(0, mstart);

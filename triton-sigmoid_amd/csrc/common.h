@@ -137,6 +137,7 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+
 // ---------------------------------------------------------------------------
 // Swizzled LDS tiles.  A [rows][D] tile of 16-bit elements is stored without
 // padding; its 16-byte chunk c of row r lives at chunk position c ^ swz(r).
@@ -218,15 +219,26 @@ template <int ROWS, int D, int NWAVES> struct DmaPlan {
     }
   }
   // base: uniform pointer to row 0 of the (batch, head) slice.
+  //
+  // The copy is issued through inline asm rather than the global_load_lds
+  // builtin: the compiler cannot tell the ring stages apart, so after the
+  // builtin it waits for the whole copy (vmcnt(0)) before the next LDS read
+  // of any stage, which serialises the prefetch with the compute it should
+  // overlap.  The kernels wait for the copy themselves (wait_dma() and a
+  // barrier) before any wave reads the stage it fills.
   __device__ __forceinline__ void issue(uint16_t *lds, const uint16_t *base, int stride_bytes,
                                         int row0, int nvalid) const {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int g = min(row0 + row[i], nvalid - 1);
       const uint32_t off = (uint32_t)g * (uint32_t)stride_bytes + (uint32_t)cbyte[i];
-      __builtin_amdgcn_global_load_lds((const char *)base + off,
-                                       (__attribute__((address_space(3))) void *)(lds + r0[i] * D),
-                                       16, 0, 0);
+      // The low 32 bits of a generic LDS pointer are its LDS offset.
+      const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + r0[i] * D));
+      // M0 holds the LDS destination; s_nop covers the M0-write -> LDS-DMA wait state.
+      asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(off), "s"(base), "{m0}"(dst)
+                   : "memory");
     }
   }
 };
