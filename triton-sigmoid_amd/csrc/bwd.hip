@@ -207,19 +207,35 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: workgroup = 4 waves x 32 keys; walks 64-query tiles of Q and dO,
-// two 32-query blocks at a time.
-//   S = Q·Kᵀ, dP = dO·Vᵀ (accumulators: lane = key column),
-//   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS with P, dS taken from the accumulators and
-//   Qᵀ, dOᵀ read from the tiles with ds_read_b64_tr_b16.
+// dK/dV: workgroup = 4 waves x 32 keys (one wave per SIMD); the
+// queries stream through a 4-stage ring of 64-query Q and dO tiles as a
+// continuous sequence of 32-query blocks g.  Per block and wave:
+//   S = Q·Kᵀ and dP = dO·Vᵀ (A: Q / dO rows from LDS, B: K / V rows held in
+//   registers; accumulators: lane = key column, registers = query rows),
+//   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS (A: dOᵀ / Qᵀ via ds_read_b64_tr_b16,
+//   B: packed P / dS words straight from the accumulator layout).
+// Region r runs, as one straight-line sequence, the S / dP MFMAs of block r,
+// the gradient MFMAs of block r-2 and the P / dS VALU work of block r-1; every
+// MFMA A operand is read from LDS eight MFMAs ahead through a rotating
+// register queue, so no MFMA waits on a fresh LDS read.  Element masks
+// (causal diagonal, seq_lens_q, pipeline fill) are applied to the packed
+// words of the few blocks that need them.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
-  constexpr int BN = 128, BMQ = 64;  // keys per workgroup, queries per LDS tile
+__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
+  constexpr int BN = 128;                 // keys per workgroup (32 per wave)
+  constexpr int BMQ = 64;                 // queries per LDS tile (two 32-query blocks)
+  constexpr int NST = 4;                  // LDS ring stages
   constexpr int NKS = D / 16, NDB = D / 32;
+  constexpr int NM = 2 * NKS + 4 * NDB;   // MFMAs per region
+  constexpr int LA = 8;                   // operand read-ahead, in MFMAs
+  constexpr int NWIN = NM / 4;            // VALU windows (four MFMAs each) per region
+  constexpr int PPW = 8 / NWIN;           // element pairs per window
+  constexpr int BAR = NM - LA;            // MFMA position of the tile barrier in odd regions
+  static_assert(NM % LA == 0 && BAR % 4 == 0, "region shape");
 
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BMQ * D];
-  __shared__ __attribute__((aligned(16))) uint16_t sO[2][BMQ * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[NST][BMQ * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];
 
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -228,7 +244,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   const int Lq = clamp_len(p.seq_q, b, p.Tq);
   const int Lk = clamp_len(p.seq_k, b, p.Tk);
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int k0 = kblk * BN, kw = k0 + w * 32, my_k = kw + l32;
 
@@ -241,9 +258,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   uint16_t *dKb = (uint16_t *)p.dk + koff;
   uint16_t *dVb = (uint16_t *)p.dv + koff;
 
+  // Causal: queries before the workgroup's first key see none of its keys.
   const int mstart = CAUSAL ? (k0 / BMQ) * BMQ : 0;
   const int mend = (k0 >= Lk) ? mstart : Lq;
   const int ntiles = mend > mstart ? (mend - mstart + BMQ - 1) / BMQ : 0;
+  const int NB = 2 * ntiles;
 
   const float scale = *p.scale;
   const float bias = p.bias[b];
@@ -262,6 +281,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       vf[s] = kok ? *(const u32x4 *)(vr + 16 * s) : zero4();
     }
   }
+  // Consume the K / V loads before the loop, so the compiler's wait for them
+  // is not placed at the loop head, where it would also wait for tile copies.
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(kf[s]), "v"(vf[s]));
+
   f32x16 dka[NDB], dva[NDB];
 #pragma unroll
   for (int d = 0; d < NDB; ++d) { dka[d] = zero16(); dva[d] = zero16(); }
@@ -271,118 +295,173 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   DmaPlan<BMQ, D, 4> dma;
   dma.init(w, lane);
   const int q_stride_bytes = (int)(p.sq_t * 2);
+  auto issue = [&](int st, int t) SIGATTN_INLINE {
+    dma.issue(sQ[st], Qb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
+    dma.issue(sO[st], dOb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
+  };
 
-  // P and dS of one 32-query block (rows qbase.., this lane's key).
-  auto pds_block = [&](const f32x16 &s, const f32x16 &dp, int qbase, uint32_t *pk, uint32_t *dsk,
-                       bool mask) SIGATTN_INLINE {
-    float pv[16], ds[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      pv[i] = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, nc));
-      const float t = pv[i] * dp[i];
-      ds[i] = __builtin_fmaf(-pv[i], t, t);
+  f32x16 sacc[2], pacc[2];       // S and dP accumulators, by block parity
+  uint32_t pw[2][8], dw[2][8];   // packed P and dS words, by block parity
+  u32x4 opq[LA];                 // A operands of the next LA MFMAs (slot = position % LA)
+  float ex[PPW][2];              // exp2 terms of the next element pairs
+
+  // A operand of MFMA m of the region whose blocks (S/dP block, gradient
+  // block) sit at tile rows kl in ring stages stc / stg.
+  auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
+    if (m < 2 * NKS) {
+      return (m % 2 == 0) ? ld_row<D>(sQ[stc], to, kl, m / 2) : ld_row<D>(sO[stc], to, kl, m / 2);
+    } else {
+      const int i = m - 2 * NKS, j = i / (2 * NDB), dbi = (i / 2) % NDB;
+      return (i % 2 == 0) ? ld_tr<D>(sO[stg], to, kl / 16 + j, dbi)
+                          : ld_tr<D>(sQ[stg], to, kl / 16 + j, dbi);
     }
-    if (mask) {
+  };
+
+  // Zeroes the P and dS entries of block g whose query lies before the
+  // block range (pipeline fill; as unsigned such queries may also wrap to
+  // huge values), at or past seq_lens_q, or (causal) before the lane's key.
+  auto mask_words = [&](int slot, int g) SIGATTN_INLINE {
+    int qbase = mstart + 32 * g;
+    asm volatile("" : "+s"(qbase));  // keeps this rare fix-up in its own branch
+    const unsigned lo = CAUSAL ? (unsigned)max(my_k, mstart) : (unsigned)mstart;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q = qbase + 8 * (i / 4) + 4 * hi + (i % 4);
-        if (q >= Lq || (CAUSAL && q < my_k)) { pv[i] = 0.0f; ds[i] = 0.0f; }
+    for (int e = 0; e < 8; ++e) {
+      const int i = 2 * e;
+      const unsigned q0 = (unsigned)(qbase + 8 * (i / 4) + 4 * hi + (i % 4));
+      const bool ok0 = q0 >= lo && q0 < (unsigned)Lq;
+      const bool ok1 = q0 + 1u >= lo && q0 + 1u < (unsigned)Lq;
+      const uint32_t m = (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
+      pw[slot][e] &= m;
+      dw[slot][e] &= m;
+    }
+  };
+  auto needs_mask = [&](int g) SIGATTN_INLINE {
+    const int qb0 = mstart + 32 * g;
+    return g < 0 || qb0 + 32 > Lq || (CAUSAL && qb0 < kw + 31);
+  };
+
+  // One region (U = r mod 8, so every slot and ring stage is static).
+  auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
+    constexpr int U = decltype(u_tag)::value;
+    constexpr int SL = U % 2;                     // parity of blocks r and r-2
+    constexpr int KL = 32 * (U % 2);              // tile rows of blocks r and r-2
+    constexpr int KLn = 32 * ((U + 1) % 2);       // tile rows of blocks r+1 and r-1
+    constexpr int STC = (U / 2) % NST;            // stage of block r
+    constexpr int STG = ((U + 6) / 2) % NST;      // stage of block r-2
+    constexpr int STCn = ((U + 1) / 2) % NST;     // stage of block r+1
+    constexpr int STGn = ((U + 7) / 2) % NST;     // stage of block r-1
+    sacc[SL] = zero16();
+    pacc[SL] = zero16();
+#pragma unroll
+    for (int win = 0; win < NWIN; ++win) {
+      if ((U % 2) == 1 && win * 4 == BAR) {
+        // Publish tile (r+1)/2 before the first read of it (the read-ahead of
+        // block r+1), then start the copy of the tile after it into the stage
+        // of the tile three back, whose last reads were two regions ago.
+        const int t1 = (r + 1) / 2;
+        if (t1 < ntiles) {
+          wait_dma();
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          if (t1 + 1 < ntiles) issue((t1 + 1) % NST, t1 + 1);
+        }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      pk[i] = Elem<T>::pack(pv[2 * i], pv[2 * i + 1]);
-      dsk[i] = Elem<T>::pack(ds[2 * i], ds[2 * i + 1]);
-    }
-  };
-
-  // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS for the two 16-query steps of block qbk.
-  auto grad_block = [&](int st, int qbk, const uint32_t *pk, const uint32_t *dsk) SIGATTN_INLINE {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const u32x4 pb = (u32x4){pk[4 * j], pk[4 * j + 1], pk[4 * j + 2], pk[4 * j + 3]};
-      const u32x4 sb = (u32x4){dsk[4 * j], dsk[4 * j + 1], dsk[4 * j + 2], dsk[4 * j + 3]};
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        dva[db] = Elem<T>::mfma(ld_tr<D>(sO[st], to, 2 * qbk + j, db), pb, dva[db]);
-        dka[db] = Elem<T>::mfma(ld_tr<D>(sQ[st], to, 2 * qbk + j, db), sb, dka[db]);
+      for (int mm = 0; mm < 4; ++mm) {
+        const int m = win * 4 + mm;
+        const u32x4 a = opq[m % LA];
+        if (m < 2 * NKS) {
+          if (m % 2 == 0) sacc[SL] = Elem<T>::mfma(a, kf[m / 2], sacc[SL]);
+          else pacc[SL] = Elem<T>::mfma(a, vf[m / 2], pacc[SL]);
+        } else {
+          const int i = m - 2 * NKS, j = i / (2 * NDB), dbi = (i / 2) % NDB;
+          if (i % 2 == 0) {
+            const u32x4 bp = (u32x4){pw[SL][4 * j], pw[SL][4 * j + 1], pw[SL][4 * j + 2], pw[SL][4 * j + 3]};
+            dva[dbi] = Elem<T>::mfma(a, bp, dva[dbi]);
+          } else {
+            const u32x4 bd = (u32x4){dw[SL][4 * j], dw[SL][4 * j + 1], dw[SL][4 * j + 2], dw[SL][4 * j + 3]};
+            dka[dbi] = Elem<T>::mfma(a, bd, dka[dbi]);
+          }
+        }
+        // Refill the slot with the operand of MFMA m + LA (next region when
+        // it wraps: S/dP block r+1, gradient block r-1).
+        if (m + LA < NM) opq[m % LA] = read_op(m + LA, STC, STG, KL);
+        else opq[m % LA] = read_op(m + LA - NM, STCn, STGn, KLn);
       }
+      // VALU: P / dS of block r-1 (parity 1-SL).  Stage B (reciprocal, dS,
+      // packing) for this window's pairs, stage A (exp2) for the next
+      // window's pairs -- or, in the last window, the first pairs of block r.
+      float nx[PPW][2];
+#pragma unroll
+      for (int pp = 0; pp < PPW; ++pp) {
+        const bool last = win + 1 == NWIN;
+        const int e = last ? pp : (win + 1) * PPW + pp;
+        const f32x16 &sv = last ? sacc[SL] : sacc[1 - SL];
+        nx[pp][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * e], nsl, nc));
+        nx[pp][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * e + 1], nsl, nc));
+      }
+#pragma unroll
+      for (int pp = 0; pp < PPW; ++pp) {
+        const int e = win * PPW + pp;
+        float pr[2], ds[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          pr[x] = __builtin_amdgcn_rcpf(1.0f + ex[pp][x]);
+          const float t = pr[x] * pacc[1 - SL][2 * e + x];
+          ds[x] = __builtin_fmaf(-pr[x], t, t);
+        }
+        pw[1 - SL][e] = Elem<T>::pack(pr[0], pr[1]);
+        dw[1 - SL][e] = Elem<T>::pack(ds[0], ds[1]);
+        asm volatile("" : "+v"(pw[1 - SL][e]), "+v"(dw[1 - SL][e]));
+      }
+#pragma unroll
+      for (int pp = 0; pp < PPW; ++pp) { ex[pp][0] = nx[pp][0]; ex[pp][1] = nx[pp][1]; }
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 4 * PPW, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if (r == 0 || needs_mask(r - 1)) mask_words(1 - SL, r - 1);
   };
 
-  // One pair of 32-query blocks (tile rows qo .. qo+63) in four regions:
-  // A S0/dP0 chains; B S1/dP1 chains || P,dS of block 0;
-  // C grads of block 0 || P,dS of block 1; D grads of block 1.
-  auto pair_step = [&](int st, int m0, int qo, bool mask) SIGATTN_INLINE {
-    f32x16 s0 = zero16(), d0 = zero16(), s1 = zero16(), d1 = zero16();
-    uint32_t p0[8], g0[8], p1[8], g1[8];
+  // Pipeline fill: blocks -2 and -1 contribute P = dS = 0; their gradient
+  // operands come from ring stage 3, zeroed here (tile 3 arrives only after
+  // region 3), so 0 * operand stays 0.
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      s0 = Elem<T>::mfma(ld_row<D>(sQ[st], to, qo, ks), kf[ks], s0);
-      d0 = Elem<T>::mfma(ld_row<D>(sO[st], to, qo, ks), vf[ks], d0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
+  for (int x = 0; x < 2; ++x) {
+    sacc[x] = zero16();
+    pacc[x] = zero16();
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      s1 = Elem<T>::mfma(ld_row<D>(sQ[st], to, qo + 32, ks), kf[ks], s1);
-      d1 = Elem<T>::mfma(ld_row<D>(sO[st], to, qo + 32, ks), vf[ks], d1);
-    }
-    pds_block(s0, d0, m0 + qo, p0, g0, mask);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    for (int e = 0; e < 8; ++e) { pw[x][e] = 0u; dw[x][e] = 0u; }
+  }
 #pragma unroll
-    for (int i = 0; i < 2 * NKS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    grad_block(st, qo / 32, p0, g0);
-    pds_block(s1, d1, m0 + qo + 32, p1, g1, mask);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 4 * NDB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    grad_block(st, qo / 32 + 1, p1, g1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 4 * NDB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // A 128-query tile = two pairs; each pair masks / skips on its own rows.
-  auto tile_step = [&](int st, int m0) SIGATTN_INLINE {
-#pragma unroll
-    for (int qo = 0; qo < BMQ; qo += 64) {
-      const int mq = m0 + qo;
-      if (CAUSAL && mq + 63 < kw) continue;  // every query of the pair precedes this wave's keys
-      pair_step(st, m0, qo, (mq + 64 > Lq) || (CAUSAL && mq < kw + 31));
-    }
-  };
-
-  auto issue = [&](int st, int m0) SIGATTN_INLINE {
-    dma.issue(sQ[st], Qb, q_stride_bytes, m0, Lq);
-    dma.issue(sO[st], dOb, q_stride_bytes, m0, Lq);
-  };
-  auto iteration = [&](int it, auto stage_tag) SIGATTN_INLINE {
-    constexpr int ST = decltype(stage_tag)::value;
-    const int m0 = mstart + it * BMQ;
+  for (int pp = 0; pp < PPW; ++pp) { ex[pp][0] = 0.0f; ex[pp][1] = 0.0f; }
+  for (int i = tid; i < BMQ * D / 8; i += 256) {
+    *(u32x4 *)&sQ[NST - 1][8 * i] = zero4();
+    *(u32x4 *)&sO[NST - 1][8 * i] = zero4();
+  }
+  if (ntiles > 0) {
+    issue(0, 0);
     wait_dma();
-    __syncthreads();
-    if (it + 1 < ntiles) issue(ST ^ 1, m0 + BMQ);
-    if (!CAUSAL || m0 + BMQ - 1 >= kw) tile_step(ST, m0);
-  };
+  }
+  __syncthreads();
+  if (ntiles > 1) issue(1, 1);
+#pragma unroll
+  for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
 
-  if (ntiles > 0) issue(0, mstart);
-  for (int it = 0; it < ntiles; it += 2) {
-    iteration(it, std::integral_constant<int, 0>{});
-    if (it + 1 < ntiles) iteration(it + 1, std::integral_constant<int, 1>{});
+  for (int r0 = 0; r0 < NB + 2; r0 += 8) {
+    region(r0 + 0, std::integral_constant<int, 0>{});
+    if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
+    if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
+    if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
+    if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
+    if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
+    if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
+    if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
   }
 
   if (my_k < p.Tk) {
