@@ -350,8 +350,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
     constexpr int STG = ((U + 6) / 2) % NST;      // stage of block r-2
     constexpr int STCn = ((U + 1) / 2) % NST;     // stage of block r+1
     constexpr int STGn = ((U + 7) / 2) % NST;     // stage of block r-1
-    sacc[SL] = zero16();
-    pacc[SL] = zero16();
 #pragma unroll
     for (int win = 0; win < NWIN; ++win) {
       if ((U % 2) == 1 && win * 4 == BAR) {
@@ -367,13 +365,16 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
           if (t1 + 1 < ntiles) issue((t1 + 1) % NST, t1 + 1);
         }
       }
+      // One wait for the window's four operands instead of one per MFMA.
+      asm volatile("" ::"v"(opq[(win * 4) % LA]), "v"(opq[(win * 4 + 1) % LA]),
+                   "v"(opq[(win * 4 + 2) % LA]), "v"(opq[(win * 4 + 3) % LA]));
 #pragma unroll
       for (int mm = 0; mm < 4; ++mm) {
         const int m = win * 4 + mm;
         const u32x4 a = opq[m % LA];
         if (m < 2 * NKS) {
-          if (m % 2 == 0) sacc[SL] = Elem<T>::mfma(a, kf[m / 2], sacc[SL]);
-          else pacc[SL] = Elem<T>::mfma(a, vf[m / 2], pacc[SL]);
+          if (m % 2 == 0) sacc[SL] = Elem<T>::mfma(a, kf[m / 2], m == 0 ? zero16() : sacc[SL]);
+          else pacc[SL] = Elem<T>::mfma(a, vf[m / 2], m == 1 ? zero16() : pacc[SL]);
         } else {
           const int i = m - 2 * NKS, j = i / (2 * NDB), dbi = (i / 2) % NDB;
           if (i % 2 == 0) {
@@ -398,19 +399,21 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
         const bool last = win + 1 == NWIN;
         const int e = last ? pp : (win + 1) * PPW + pp;
         const f32x16 &sv = last ? sacc[SL] : sacc[1 - SL];
-        nx[pp][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * e], nsl, nc));
-        nx[pp][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * e + 1], nsl, nc));
+        nx[pp][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(sv[2 * e]), nsl, nc));
+        nx[pp][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(sv[2 * e + 1]), nsl, nc));
       }
 #pragma unroll
       for (int pp = 0; pp < PPW; ++pp) {
         const int e = win * PPW + pp;
-        float pr[2], ds[2];
+        // Written stage by stage for both elements, so each transcendental
+        // result is not consumed by the very next instruction.
+        float pr[2], t[2], ds[2];
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          pr[x] = __builtin_amdgcn_rcpf(1.0f + ex[pp][x]);
-          const float t = pr[x] * pacc[1 - SL][2 * e + x];
-          ds[x] = __builtin_fmaf(-pr[x], t, t);
-        }
+        for (int x = 0; x < 2; ++x) pr[x] = __builtin_amdgcn_rcpf(1.0f + ex[pp][x]);
+#pragma unroll
+        for (int x = 0; x < 2; ++x) t[x] = pr[x] * acc_read(pacc[1 - SL][2 * e + x]);
+#pragma unroll
+        for (int x = 0; x < 2; ++x) ds[x] = __builtin_fmaf(-pr[x], t[x], t[x]);
         pw[1 - SL][e] = Elem<T>::pack(pr[0], pr[1]);
         dw[1 - SL][e] = Elem<T>::pack(ds[0], ds[1]);
         asm volatile("" : "+v"(pw[1 - SL][e]), "+v"(dw[1 - SL][e]));

@@ -138,6 +138,18 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 
+// Reads one accumulator element that lives in an AGPR into a VGPR at this
+// point of the instruction stream.  The MFMA accumulators of the kernels sit
+// in AGPRs; left to itself the compiler copies a whole accumulator to VGPRs
+// in one burst (stalling the matrix pipe and holding 16 extra VGPRs), while
+// this spreads the copies over the VALU work that consumes them.  Callers
+// only read elements whose MFMA finished several MFMAs earlier.
+__device__ __forceinline__ float acc_read(float v) {
+  float out;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(out) : "a"(v));
+  return out;
+}
+
 // ---------------------------------------------------------------------------
 // Swizzled LDS tiles.  A [rows][D] tile of 16-bit elements is stored without
 // padding; its 16-byte chunk c of row r lives at chunk position c ^ swz(r).
