@@ -488,12 +488,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
   }
 }
 
-#define SIGATTN_BWD_LAUNCHER(NAME, KERNEL, ROWBLK, ROWS)                                    \
+#define SIGATTN_BWD_LAUNCHER(NAME, KERNEL, ROWBLK, ROWS, THREADS)                           \
   template <typename T, int D>                                                              \
   static void NAME##_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {           \
     KParams p = kp;                                                                         \
     p.nblk = ((ROWS) + (ROWBLK) - 1) / (ROWBLK);                                            \
-    const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(256);                            \
+    const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(THREADS);                        \
     if (causal) {                                                                           \
       if (sm) KERNEL<T, D, true, true><<<grid, block, 0, st>>>(p);                          \
       else KERNEL<T, D, true, false><<<grid, block, 0, st>>>(p);                            \
@@ -512,8 +512,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
     }                                                                                       \
   }
 
-SIGATTN_BWD_LAUNCHER(launch_bwd_dq_mfma, bwd_dq_kernel, 128, p.Tq)
-SIGATTN_BWD_LAUNCHER(launch_bwd_dkdv_mfma, bwd_dkdv_kernel, 128, p.Tk)
+SIGATTN_BWD_LAUNCHER(launch_bwd_dq_mfma, bwd_dq_kernel, 128, p.Tq, 256)
+SIGATTN_BWD_LAUNCHER(launch_bwd_dkdv_mfma, bwd_dkdv_kernel, 128, p.Tk, 256)
 
 #undef SIGATTN_BWD_LAUNCHER
 
