@@ -12,6 +12,12 @@ FLOPs (algorithmic, extending the reference's benchmarks/benchmark_sigmoid.py
 fwd+bwd = 14·D; causal counts L²/2 pairs.  Recomputed or masked work is not
 credited.
 
+Padded workloads (--config c4 / c5, BASELINE.json configs[3] / [4]): seq_lens_q
+= seq_lens_k ~ U[lo, Lmax] per batch element from the same seeded generator,
+padding rows filled with N(0,1) noise; FLOPs count only valid (query, key)
+pairs, and the same run times the dense kernels at the full shape to report
+the padded path's TFLOPS per valid token as a fraction of dense.
+
 Prints ONE JSON line on stdout; details go to stderr.
 """
 
@@ -38,6 +44,12 @@ CONFIGS = {
     "c2c": dict(B=2, L=1024, H=8, D=64, dtype="float16", causal=True),
     "c3": dict(B=4, L=4096, H=16, D=128, dtype="bfloat16", causal=True),
     "c3nc": dict(B=4, L=4096, H=16, D=128, dtype="bfloat16", causal=False),
+    # padded fp16, seq_lens ~ U[512, 2048], causal.
+    "c4": dict(B=8, L=2048, H=8, D=64, dtype="float16", causal=True, padded=True, lo=512),
+    # padded bf16 long context, seq_lens ~ U[1024, 8192],
+    # non-causal, through torch.compile(sigmoid_attention_padded).
+    "c5": dict(B=4, L=8192, H=12, D=64, dtype="bfloat16", causal=False, padded=True, lo=1024,
+               compiled=True),
 }
 
 
@@ -57,6 +69,22 @@ def make_inputs(cfg, device):
     return [torch.randn(shape, generator=g, dtype=torch.float32).to(dtype).to(device) for _ in range(4)]
 
 
+def make_seq_lens(cfg, device):
+    """Per-batch valid lengths ~ U[lo, L] (int32) for the padded configs, else None."""
+    import torch
+    if not cfg.get("padded"):
+        return None
+    g = torch.Generator().manual_seed(1)
+    return torch.randint(cfg["lo"], cfg["L"] + 1, (cfg["B"],), generator=g, dtype=torch.int32).to(device)
+
+
+def valid_pairs(cfg, seq_lens) -> float:
+    """(query, key) pairs the kernels must compute, summed over batch and heads."""
+    if seq_lens is None:
+        return pairs(cfg["L"], cfg["causal"]) * cfg["B"] * cfg["H"]
+    return sum(pairs(int(n), cfg["causal"]) for n in seq_lens.tolist()) * cfg["H"]
+
+
 def time_region(fn, iters: int, warmup: int):
     """Median per-call ms over `iters` calls bracketed by events on the current stream."""
     import torch
@@ -74,7 +102,7 @@ def time_region(fn, iters: int, warmup: int):
     return statistics.median(times), times
 
 
-def kernel_times(cfg, q, k, v, do, iters: int):
+def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None):
     """Average duration of each kernel, launched one at a time through the C ABI
     on torch's current stream and bracketed by HIP events on that stream."""
     import ctypes
@@ -82,9 +110,12 @@ def kernel_times(cfg, q, k, v, do, iters: int):
     from triton_sigmoid import _capi
     lib = _capi.load_library()
     B, L, H, D = q.shape
-    bias = torch.full((B,), -math.log(L), dtype=torch.float32, device=q.device)
+    if seq_lens is None:
+        bias = torch.full((B,), -math.log(L), dtype=torch.float32, device=q.device)
+    else:
+        bias = -torch.log(seq_lens.float())
     scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=q.device)
-    pr = _capi._problem(q, k, v, bias, None, scale, None, None, cfg["causal"])
+    pr = _capi._problem(q, k, v, bias, None, scale, seq_lens, seq_lens, cfg["causal"])
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     calls = {
@@ -163,6 +194,17 @@ def load_traffic(kernel: str, config: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+def workload_name(name, cfg) -> str:
+    shape = f"B={cfg['B']} L={cfg['L']} H={cfg['H']} D={cfg['D']} {cfg['dtype']} causal={cfg['causal']}"
+    if cfg.get("padded"):
+        how = "torch.compile(sigmoid_attention_padded)" if cfg.get("compiled") else "sigmoid_attention_padded"
+        tag = {"c4": " (BASELINE.json configs[3])", "c5": " (BASELINE.json configs[4])"}.get(name, "")
+        return f"padded sigmoid attention fwd+bwd via {how}, {shape}, seq_lens ~ U[{cfg['lo']}, {cfg['L']}]{tag}"
+    tag = {"c3": " (BASELINE.json configs[2])", "c2": " (BASELINE.json configs[1])",
+           "c2c": " (BASELINE.json configs[1])"}.get(name, "")
+    return f"dense sigmoid attention fwd+bwd, {shape}{tag}"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,16 +235,25 @@ def main():
     for t in (q, k, v):
         t.requires_grad_(True)
     B, L, H, D, causal = cfg["B"], cfg["L"], cfg["H"], cfg["D"], cfg["causal"]
-    P = pairs(L, causal) * B * H
+    sl = make_seq_lens(cfg, dev)
+    P = valid_pairs(cfg, sl)
     fwd_flops, fb_flops = 4 * D * P, 14 * D * P
+
+    if sl is None:
+        attn = lambda: ts.sigmoid_attention(q, k, v, is_causal=causal)
+    else:
+        padded = ts.sigmoid_attention_padded
+        if cfg.get("compiled"):
+            padded = torch.compile(ts.sigmoid_attention_padded, fullgraph=True)
+        attn = lambda: padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl, is_causal=causal)
 
     def fwd():
         with torch.no_grad():
-            ts.sigmoid_attention(q, k, v, is_causal=causal)
+            attn()
 
     def step():
         q.grad = k.grad = v.grad = None
-        o = ts.sigmoid_attention(q, k, v, is_causal=causal)
+        o = attn()
         o.backward(do)
 
     # Whole-job timing of K fwd+bwd steps.
@@ -218,7 +269,7 @@ def main():
 
     fwd_ms, _ = time_region(fwd, iters=max(10, args.steps), warmup=3)
     fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
-    kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, args.steps))
+    kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, args.steps), seq_lens=sl)
     credit = {"fwd": 4 * D * P, "bwd_dq": 2 * D * P, "bwd_dkdv": 8 * D * P}
     dominant = max(kt, key=kt.get)
     achieved = credit[dominant] / (kt[dominant] * 1e-3) / 1e12
@@ -227,6 +278,24 @@ def main():
     log(f"[bench] step {ms_step:.3f} ms -> fwd+bwd {fb_tflops:.1f} TFLOPS ({100 * fb_tflops / PEAK_BF16_TFLOPS:.1f}% peak)")
     log(f"[bench] fwd {fwd_ms:.3f} ms -> {fwd_tflops:.1f} TFLOPS; kernels (ms): "
         + ", ".join(f"{n}={t:.3f}" for n, t in kt.items()))
+
+    padded_info = None
+    if sl is not None:
+        # Dense kernels at the full shape, same run: the padded path's TFLOPS
+        # per valid token as a fraction of dense TFLOPS.
+        kd = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, args.steps))
+        Pd = pairs(L, causal) * B * H
+        dense_tf = 14 * D * Pd / (sum(kd.values()) * 1e-3) / 1e12
+        padded_tf = 14 * D * P / (sum(kt.values()) * 1e-3) / 1e12
+        padded_info = {
+            "seq_lens": sl.tolist(),
+            "valid_pair_fraction": round(P / Pd, 4),
+            "padded_kernel_tflops": round(padded_tf, 2),
+            "dense_kernel_tflops": round(dense_tf, 2),
+            "padded_vs_dense": round(padded_tf / dense_tf, 4),
+            "note": "kernel sums (fwd + dQ + dK/dV) through the C ABI; padded counts valid pairs only",
+        }
+        log(f"[bench] padded {padded_info}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -247,9 +316,7 @@ def main():
         "dtype": "bf16" if cfg["dtype"] == "bfloat16" else "fp16",
         "data": "synthetic: q,k,v,dO ~ N(0,1) from torch.Generator seed 0",
         "config": {
-            "workload": f"dense sigmoid attention fwd+bwd, B={B} L={L} H={H} D={D} "
-                        f"{cfg['dtype']} causal={causal} (BASELINE.json configs[2])" if args.config == "c3"
-                        else f"dense sigmoid attention fwd+bwd, B={B} L={L} H={H} D={D} {cfg['dtype']} causal={causal}",
+            "workload": workload_name(args.config, cfg),
             "batch": B, "seq_len": L, "heads": H, "head_dim": D, "causal": causal,
         },
         "pct_of_peak": round(100 * fb_tflops / PEAK_BF16_TFLOPS, 2),
@@ -268,6 +335,8 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if padded_info is not None:
+        line["padded"] = padded_info
     print(json.dumps(line), flush=True)
 
 
