@@ -9,7 +9,6 @@
 
 #include <climits>
 #include <cstdint>
-#include <mutex>
 
 #include "../../include/sigattn.h"
 #include "launch.h"
@@ -63,33 +62,6 @@ bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
 
 int launch_status() {
   return hipGetLastError() == hipSuccess ? SIGATTN_OK : SIGATTN_ERR_LAUNCH;
-}
-
-// The dQ and dK/dV kernels are independent.  sigattn_bwd forks the dQ kernel
-// onto a library-owned side stream (default priority, one per device, created
-// on first use) and joins it back with events, so each kernel's tail overlaps
-// the other's work instead of idling the GPU.  Fork/join through events is
-// valid under stream capture.
-constexpr int kMaxDevices = 64;
-struct SideStream {
-  std::once_flag once;
-  std::mutex mu;  // one fork/launch/join sequence at a time (the events are shared)
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-  bool ok = false;
-};
-SideStream g_side[kMaxDevices];
-
-SideStream *side_stream() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  SideStream &s = g_side[dev];
-  std::call_once(s.once, [&s] {
-    s.ok = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess &&
-           hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
-  });
-  return s.ok ? &s : nullptr;
 }
 
 }  // namespace
@@ -176,28 +148,17 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   const bool mfma = use_mfma(p, ptrs, 7);
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
   (void)hipGetLastError();
-  SideStream *side = (need_dq && need_dkdv) ? side_stream() : nullptr;
-  std::unique_lock<std::mutex> lock;
-  if (side != nullptr) lock = std::unique_lock<std::mutex>(side->mu);
-  hipStream_t dq_stream = st;
-  if (side != nullptr) {
-    if (hipEventRecord(side->fork, st) != hipSuccess ||
-        hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)
-      return SIGATTN_ERR_LAUNCH;
-    dq_stream = side->stream;
-  }
+  // Both kernels go on the caller's stream, one after the other: each fills
+  // the GPU on its own and they cannot share a CU (their LDS footprints add
+  // up to more than one CU holds), so running them concurrently on two
+  // streams only made both slower (measured).
   if (need_dq) {
-    if (mfma) sigattn::launch_bwd_dq_mfma(k, p->dtype, (int)p->D, causal, sm, dq_stream);
-    else sigattn::launch_bwd_dq_generic(k, p->dtype, (int)p->D, causal, dq_stream);
+    if (mfma) sigattn::launch_bwd_dq_mfma(k, p->dtype, (int)p->D, causal, sm, st);
+    else sigattn::launch_bwd_dq_generic(k, p->dtype, (int)p->D, causal, st);
   }
   if (need_dkdv) {
     if (mfma) sigattn::launch_bwd_dkdv_mfma(k, p->dtype, (int)p->D, causal, sm, st);
     else sigattn::launch_bwd_dkdv_generic(k, p->dtype, (int)p->D, causal, st);
-  }
-  if (side != nullptr) {
-    if (hipEventRecord(side->join, side->stream) != hipSuccess ||
-        hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
-      return SIGATTN_ERR_LAUNCH;
   }
   return launch_status();
 }
