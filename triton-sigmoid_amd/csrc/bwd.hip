@@ -41,11 +41,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? 2 * BN : 4];
 
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  int qb = blockIdx.x / BH;
-  if (CAUSAL) qb = p.nblk - 1 - qb;
-  const int b = bh / p.H, h = bh % p.H;
+  int b, h, qb;
+  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, true)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, p.seq_k, p.Tk);
+    b = it.b, h = it.h, qb = it.blk;
+  } else {
+    const int BH = p.B * p.H;
+    const int bh = blockIdx.x % BH;
+    qb = blockIdx.x / BH;
+    if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
+    b = bh / p.H, h = bh % p.H;
+  }
   const int Lq = clamp_len(p.seq_q, b, p.Tq);
   const int Lk = clamp_len(p.seq_k, b, p.Tk);
 
@@ -237,10 +244,17 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sQ[NST][BMQ * D];
   __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];
 
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  const int kblk = blockIdx.x / BH;  // causal: low key blocks carry the most work and come first
-  const int b = bh / p.H, h = bh % p.H;
+  int b, h, kblk;
+  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_k, p.Tk, BN, p.nblk, false)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_k, p.Tk, BN, p.nblk, p.seq_q, p.Tq);
+    b = it.b, h = it.h, kblk = it.blk;
+  } else {
+    const int BH = p.B * p.H;
+    const int bh = blockIdx.x % BH;
+    kblk = blockIdx.x / BH;  // causal: low key blocks carry the most work and come first
+    b = bh / p.H, h = bh % p.H;
+  }
   const int Lq = clamp_len(p.seq_q, b, p.Tq);
   const int Lk = clamp_len(p.seq_k, b, p.Tk);
 

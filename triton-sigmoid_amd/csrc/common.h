@@ -57,6 +57,92 @@ __device__ __forceinline__ int clamp_len(const int32_t *lens, int b, int T) {
   return L < 0 ? 0 : (L > T ? T : L);
 }
 
+// ---------------------------------------------------------------------------
+// Work-item order.  A kernel's grid covers (row block, batch, head) items of
+// its stationary sequence (queries for the forward and dQ, keys for dK/dV).
+// The hardware deals workgroup ids round-robin over the 8 XCDs and each XCD
+// starts them in id order, so ids sorted by decreasing work give every XCD an
+// even, heaviest-first share.  Dense grids already are in that order (all
+// items equal, or causal row blocks heaviest first); for padded batches the
+// work depends on each batch's lengths, so WorkOrder re-derives the item of
+// workgroup `id` from seq_lens on the device (no host sync):
+//   * by_stream: items of longer streamed sequences first (non-causal: every
+//     row block of batch b costs its full streamed length);
+//   * by_level: row-block levels in the given direction (causal: the cost
+//     grows with the query block, or shrinks with the key block), the batches
+//     valid at a level in index order, heads fastest.
+// Padding items (row block past a batch's length) come after all valid items,
+// batch by batch; their workgroups only write the zero rows.  Every lane of
+// every wave computes the same answer (lane j holds batch j), so B is limited
+// to 64; callers keep the dense order beyond that.
+struct WorkItem {
+  int b, h, blk;
+};
+
+struct WorkOrder {
+  // Row blocks of batch `lane` (0 for lanes past B).
+  static __device__ __forceinline__ int row_blocks(const int32_t *rows, int T, int RB, int B, int lane) {
+    if (lane >= B) return 0;
+    return (clamp_len(rows, lane, T) + RB - 1) / RB;
+  }
+  static __device__ __forceinline__ int kth_set_bit(uint64_t m, int k) {
+    for (int t = 0; t < k; ++t) m &= m - 1;
+    return __builtin_ctzll(m);
+  }
+  // Padding item j (0-based, after all valid items): batches in index order,
+  // row blocks nv..nlev-1, heads fastest.
+  static __device__ __forceinline__ WorkItem padding(int j, int B, int H, int nv, int nlev) {
+    const int lane = __lane_id();
+    const int cnt = lane < B ? (nlev - nv) * H : 0;
+    int start = 0;
+    for (int k = 0; k < B; ++k) start += k < lane ? __builtin_amdgcn_readlane(cnt, k) : 0;
+    const uint64_t m = __ballot(lane < B && j >= start && j < start + cnt);
+    const int b = m != 0 ? __builtin_ctzll(m) : 0;
+    const int r = j - __builtin_amdgcn_readlane(start, b);
+    return WorkItem{b, r % H, __builtin_amdgcn_readlane(nv, b) + r / H};
+  }
+  static __device__ __forceinline__ WorkItem by_stream(int id, int B, int H, const int32_t *rows, int Trows,
+                                                       int RB, int nlev, const int32_t *stream, int Tstream) {
+    const int lane = __lane_id();
+    const int nv = row_blocks(rows, Trows, RB, B, lane);
+    const int key = lane < B ? clamp_len(stream, lane, Tstream) : -1;
+    const int cnt = nv * H;
+    int rank = 0, total = 0;
+    for (int k = 0; k < B; ++k) {
+      const int kk = __builtin_amdgcn_readlane(key, k);
+      rank += (kk > key || (kk == key && k < lane)) ? 1 : 0;
+      total += __builtin_amdgcn_readlane(cnt, k);
+    }
+    if (id >= total) return padding(id - total, B, H, nv, nlev);
+    int start = 0;
+    for (int k = 0; k < B; ++k) {
+      const int rk = __builtin_amdgcn_readlane(rank, k), ck = __builtin_amdgcn_readlane(cnt, k);
+      start += rk < rank ? ck : 0;
+    }
+    const uint64_t m = __ballot(lane < B && id >= start && id < start + cnt);
+    const int b = __builtin_ctzll(m);
+    const int r = id - __builtin_amdgcn_readlane(start, b);
+    return WorkItem{b, r % H, r / H};
+  }
+  static __device__ __forceinline__ WorkItem by_level(int id, int B, int H, const int32_t *rows, int Trows,
+                                                      int RB, int nlev, bool descending) {
+    const int lane = __lane_id();
+    const int nv = row_blocks(rows, Trows, RB, B, lane);
+    int base = 0;
+    for (int t = 0; t < nlev; ++t) {
+      const int lev = descending ? nlev - 1 - t : t;
+      const uint64_t m = __ballot(nv > lev);
+      const int cnt = __builtin_popcountll(m) * H;
+      if (id < base + cnt) {
+        const int r = id - base;
+        return WorkItem{kth_set_bit(m, r / H), r % H, lev};
+      }
+      base += cnt;
+    }
+    return padding(id - base, B, H, nv, nlev);
+  }
+};
+
 // sigmoid(s*scale + c) given x = s*(-scale*log2e) + (-c*log2e) (one FMA
 // before this call).  Hardware exp2 and reciprocal; x = +inf gives exactly 0.
 __device__ __forceinline__ float sigmoid_from_neg_log2(float x) {

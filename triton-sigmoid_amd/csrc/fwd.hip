@@ -32,11 +32,11 @@
 
 namespace sigattn {
 
-template <typename T, int D, int NCB, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(256 * (2 / NCB), 1) void fwd_mfma_kernel(const KParams p) {
-  constexpr int NWV = 8 / NCB;          // waves per workgroup (NCB = 1: two per SIMD)
+template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
+__global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) {
+  // NWV waves per workgroup (8: two per SIMD), NCB 32-query column blocks each.
   constexpr int QW = 32 * NCB;          // queries per wave
-  constexpr int BM = NWV * QW;          // queries per workgroup (256)
+  constexpr int BM = NWV * QW;          // queries per workgroup
   constexpr int BN = 64;                // keys per LDS tile (two 32-key blocks)
   constexpr int NST = 4;                // LDS ring stages
   constexpr int NKS = D / 16;           // MFMA k-steps over the head dim
@@ -51,11 +51,18 @@ __global__ __launch_bounds__(256 * (2 / NCB), 1) void fwd_mfma_kernel(const KPar
   __shared__ __attribute__((aligned(16))) uint16_t sV[NST][BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? NST * BN : 4];
 
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  int qb = blockIdx.x / BH;
-  if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
-  const int b = bh / p.H, h = bh % p.H;
+  int b, h, qb;
+  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, true)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, p.seq_k, p.Tk);
+    b = it.b, h = it.h, qb = it.blk;
+  } else {
+    const int BH = p.B * p.H;
+    const int bh = blockIdx.x % BH;
+    qb = blockIdx.x / BH;
+    if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
+    b = bh / p.H, h = bh % p.H;
+  }
 
   const int Lq = clamp_len(p.seq_q, b, p.Tq);
   const int Lk = clamp_len(p.seq_k, b, p.Tk);
@@ -329,20 +336,29 @@ __global__ __launch_bounds__(256 * (2 / NCB), 1) void fwd_mfma_kernel(const KPar
 #define SIGATTN_FWD_NCB 1
 #endif
 
-template <typename T, int D>
-static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
-  constexpr int NCB = SIGATTN_FWD_NCB, BM = 256;
+template <typename T, int D, int NWV>
+static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
+  constexpr int NCB = SIGATTN_FWD_NCB, BM = NWV * 32 * NCB;
   KParams p = kp;
   p.nblk = (p.Tq + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nblk * p.B * p.H));
-  const dim3 block(256 * (2 / NCB));
+  const dim3 block(64 * NWV);
   if (causal) {
-    if (scoremod) fwd_mfma_kernel<T, D, NCB, true, true><<<grid, block, 0, st>>>(p);
-    else fwd_mfma_kernel<T, D, NCB, true, false><<<grid, block, 0, st>>>(p);
+    if (scoremod) fwd_mfma_kernel<T, D, NWV, NCB, true, true><<<grid, block, 0, st>>>(p);
+    else fwd_mfma_kernel<T, D, NWV, NCB, true, false><<<grid, block, 0, st>>>(p);
   } else {
-    if (scoremod) fwd_mfma_kernel<T, D, NCB, false, true><<<grid, block, 0, st>>>(p);
-    else fwd_mfma_kernel<T, D, NCB, false, false><<<grid, block, 0, st>>>(p);
+    if (scoremod) fwd_mfma_kernel<T, D, NWV, NCB, false, true><<<grid, block, 0, st>>>(p);
+    else fwd_mfma_kernel<T, D, NWV, NCB, false, false><<<grid, block, 0, st>>>(p);
   }
+}
+
+template <typename T, int D>
+static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
+#ifdef SIGATTN_FWD_SMALL_WG
+  launch_fwd_w<T, D, 4 / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
+#else
+  launch_fwd_w<T, D, 8 / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
+#endif
 }
 
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
