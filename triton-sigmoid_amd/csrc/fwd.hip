@@ -71,7 +71,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int q0 = qb * BM;
-  const int qw = q0 + w * QW;       // this wave's first query
+  // Query slot of the wave.  With eight waves, waves w and w+4 share a SIMD;
+  // giving them complementary slots (w and 7-w) evens out the per-SIMD work of
+  // causal diagonal workgroups once waves stop at their own last key block.
+  const int slot = (NWV == 8 && w >= 4) ? 11 - w : w;
+  const int qw = q0 + slot * QW;    // this wave's first query
   const int myq0 = qw + l32;        // this lane's query in column block 0 (block c: +32c)
 
   const uint16_t *Qb = (const uint16_t *)p.q + (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
@@ -294,15 +298,34 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
 #pragma unroll
   for (int o = 0; o < LA; ++o) opq[o] = read_op(o, 0, NST - 1, 0);
 
-  for (int r0 = 0; r0 < NB + 2; r0 += 8) {
+  // This wave computes only up to its own last visible key block (causal) and
+  // not at all past seq_lens_q; afterwards it only takes part in the tile
+  // barriers and copies, leaving its SIMD to the other wave there.
+  int NBw = NB;
+  if (CAUSAL) NBw = min(NBw, (qw + QW - 1) / 32 + 1);
+  if (qw >= Lq) NBw = 0;
+  const int RW = NBw > 0 ? NBw + 2 : 0;
+  for (int r0 = 0; r0 < RW; r0 += 8) {
     region(r0 + 0, std::integral_constant<int, 0>{});
-    if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
-    if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
-    if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
-    if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
-    if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
-    if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
-    if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
+    if (r0 + 1 < RW) region(r0 + 1, std::integral_constant<int, 1>{});
+    if (r0 + 2 < RW) region(r0 + 2, std::integral_constant<int, 2>{});
+    if (r0 + 3 < RW) region(r0 + 3, std::integral_constant<int, 3>{});
+    if (r0 + 4 < RW) region(r0 + 4, std::integral_constant<int, 4>{});
+    if (r0 + 5 < RW) region(r0 + 5, std::integral_constant<int, 5>{});
+    if (r0 + 6 < RW) region(r0 + 6, std::integral_constant<int, 6>{});
+    if (r0 + 7 < RW) region(r0 + 7, std::integral_constant<int, 7>{});
+  }
+  // The rest of the workgroup's regions: the same barriers and copies.
+  for (int r = RW | 1; r < NB + 2; r += 2) {
+    const int u = (r + 1) / 2;
+    if (u < ntiles) {
+      wait_dma();
+      if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (u + 1 < ntiles) issue((u + 1) % NST, u + 1);
+    }
   }
 
   // Oᵀ accumulators -> O rows (4 consecutive d per 8-byte store).
