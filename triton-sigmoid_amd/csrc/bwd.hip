@@ -229,13 +229,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 // words of the few blocks that need them.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(const KParams p) {
+__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
   constexpr int BN = 128;                 // keys per workgroup (32 per wave)
   constexpr int BMQ = 64;                 // queries per LDS tile (two 32-query blocks)
   constexpr int NST = 4;                  // LDS ring stages
   constexpr int NKS = D / 16, NDB = D / 32;
   constexpr int NM = 2 * NKS + 4 * NDB;   // MFMAs per region
-  constexpr int LA = 8;                   // operand read-ahead, in MFMAs
+  constexpr int LA = D == 64 ? 4 : 8;     // operand read-ahead, in MFMAs
   constexpr int NWIN = NM / 4;            // VALU windows (four MFMAs each) per region
   constexpr int PPW = 8 / NWIN;           // element pairs per window
   constexpr int BAR = NM - LA;            // MFMA position of the tile barrier in odd regions
