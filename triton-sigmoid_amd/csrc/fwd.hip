@@ -375,13 +375,13 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
   }
 }
 
+// D = 128: one workgroup of eight waves per CU (128 KB of LDS).  D = 64: the
+// ring takes 64 KB, so two workgroups of four waves share a CU -- the same two
+// waves per SIMD in half-size work units, which balance better on small or
+// ragged (padded) batches.
 template <typename T, int D>
 static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
-#ifdef SIGATTN_FWD_SMALL_WG
-  launch_fwd_w<T, D, 4 / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
-#else
-  launch_fwd_w<T, D, 8 / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
-#endif
+  launch_fwd_w<T, D, (D == 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
 }
 
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
