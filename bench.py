@@ -102,6 +102,43 @@ def time_region(fn, iters: int, warmup: int):
     return statistics.median(times), times
 
 
+def bench_like_reference(fn, warmup_ms: float = 100.0, rep_ms: float = 250.0, grad_to_none=()):
+    """Median ms per call, timed the way the reference's sweep times it
+    (benchmarks/benchmark_sigmoid.py:249, triton.testing.do_bench with
+    warmup=100 ms, rep=250 ms, return_mode='median'): call counts from a
+    5-call estimate, and before every timed call the gradients are reset and
+    a 512 MiB buffer is zeroed so no operand is still in the L2 or the
+    256 MB last-level cache; calls are queued back to back and the events
+    read after one final synchronisation."""
+    import torch
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(5):
+        flush.zero_()
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    est = s.elapsed_time(e) / 5
+    n_warm, n_rep = max(1, int(warmup_ms / est)), max(1, int(rep_ms / est))
+    for _ in range(n_warm):
+        fn()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    for i in range(n_rep):
+        for t in grad_to_none:
+            t.grad = None
+        flush.zero_()
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    del flush
+    return statistics.median(a.elapsed_time(b) for a, b in zip(starts, ends))
+
+
 def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None):
     """Average duration of each kernel, launched one at a time through the C ABI
     on torch's current stream and bracketed by HIP events on that stream."""
@@ -194,6 +231,66 @@ def load_traffic(kernel: str, config: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+# The reference's published chart (benchmarks/results/H100/tflops_comparison.png,
+# read off the chart +-5 TFLOPS): bf16, non-causal, sigmoid_bias = 0,
+# B = 16384/L, H = 2048/D; "bwd" = backward-only time credited with 2.5x the
+# forward FLOPs (benchmarks/benchmark_sigmoid.py:193,202,232,252-260).
+H100_CHART = {
+    ("fwd", 64, 0): [347, 381, 395, 423, 437, 445], ("bwd", 64, 0): [270, 294, 293, 309, 316, 325],
+    ("fwd", 128, 0): [371, 435, 466, 479, 486, 514], ("bwd", 128, 0): [278, 319, 334, 364, 367, 370],
+    ("fwd", 64, 25): [300, 350, 377, 411, 416, 428], ("bwd", 64, 25): [231, 253, 274, 285, 262, 300],
+    ("fwd", 128, 25): [312, 365, 380, 445, 428, 479], ("bwd", 128, 25): [244, 283, 304, 327, 326, 354],
+}
+SWEEP_L = [512, 1024, 2048, 4096, 8192, 16384]
+
+
+def sweep():
+    """The reference benchmark's grid (benchmarks/benchmark_sigmoid.py:193-260) on
+    this GPU: D in {64, 128}, L in SWEEP_L with B = 16384/L and H = 2048/D, bf16,
+    non-causal, sigmoid_bias = 0, padding 0 % (dense API), 25 % and 50 % (padded
+    API, seq_lens ~ U[(1 - p) L, L] from a seeded CPU generator,
+    benchmarks/benchmark_sigmoid.py:91-93); fwd and backward-only
+    (o.backward(dO, retain_graph=True)), timed by bench_like_reference.
+    The H100 chart has no 50 % panel, so those rows carry no comparison."""
+    import torch
+    import triton_sigmoid as ts
+    dev = torch.device("cuda", 0)
+    rows = []
+    for hd in (64, 128):
+        for pad in (0, 25, 50):
+            for li, L in enumerate(SWEEP_L):
+                B, H = 16384 // L, 2048 // hd
+                g = torch.Generator().manual_seed(L * 1000 + hd * 10 + pad)
+                q, k, v = (torch.randn((B, L, H, hd), generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+                           for _ in range(3))
+                if pad:
+                    lo = max(1, int(L * (1 - pad / 100)))
+                    sl = torch.randint(lo, L + 1, (B,), generator=g, dtype=torch.int32).to(dev)
+                    attn = lambda: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl,
+                                                               is_causal=False, sigmoid_bias=0.0)
+                    flops_fwd = 4 * H * hd * float((sl.double() ** 2).sum().item())
+                else:
+                    attn = lambda: ts.sigmoid_attention(q, k, v, sigmoid_bias=0.0)
+                    flops_fwd = 4.0 * B * H * L * L * hd
+                ms_f = bench_like_reference(attn, grad_to_none=(q, k, v))
+                o = attn()
+                do = torch.randn(o.shape, generator=g).to(torch.bfloat16).to(dev)
+                ms_b = bench_like_reference(lambda: o.backward(do, retain_graph=True), grad_to_none=(q, k, v))
+                h100 = {m: H100_CHART[(m, hd, pad)][li] if (m, hd, pad) in H100_CHART else None
+                        for m in ("fwd", "bwd")}
+                row = {"D": hd, "L": L, "B": B, "H": H, "padding_pct": pad,
+                       "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
+                       "fwd_tflops": round(flops_fwd / ms_f / 1e9, 1),
+                       "bwd_tflops": round(2.5 * flops_fwd / ms_b / 1e9, 1),
+                       "h100_fwd": h100["fwd"], "h100_bwd": h100["bwd"]}
+                rows.append(row)
+                log(f"[sweep] D={hd} L={L} B={B} H={H} pad={pad}%: fwd {row['fwd_tflops']} TFLOPS "
+                    f"(H100 {row['h100_fwd']}), bwd {row['bwd_tflops']} (H100 {row['h100_bwd']})")
+                del q, k, v, o, do
+                torch.cuda.empty_cache()
+    return rows
+
+
 def workload_name(name, cfg) -> str:
     shape = f"B={cfg['B']} L={cfg['L']} H={cfg['H']} D={cfg['D']} {cfg['dtype']} causal={cfg['causal']}"
     if cfg.get("padded"):
@@ -214,9 +311,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the reference benchmark's L/D/padding grid, beside its published H100 chart")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.sweep:
+        rows = sweep()
+        print(json.dumps({"metric": "reference benchmark grid: fwd and bwd-only TFLOPS, bf16 non-causal",
+                          "unit": "TFLOPS", "rows": rows}), flush=True)
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
