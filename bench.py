@@ -24,6 +24,7 @@ Prints ONE JSON line on stdout; details go to stderr.
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -139,9 +140,11 @@ def bench_like_reference(fn, warmup_ms: float = 100.0, rep_ms: float = 250.0, gr
     return statistics.median(a.elapsed_time(b) for a, b in zip(starts, ends))
 
 
-def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None):
+def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
     """Average duration of each kernel, launched one at a time through the C ABI
-    on torch's current stream and bracketed by HIP events on that stream."""
+    on torch's current stream and bracketed by HIP events on that stream.
+    packed=True runs the same sequences in the packed [rows, H, D] layout
+    (cu_seqlens = [0, cumsum(seq_lens)]) instead of the padded one."""
     import ctypes
     import torch
     from triton_sigmoid import _capi
@@ -152,7 +155,14 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None):
     else:
         bias = -torch.log(seq_lens.float())
     scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=q.device)
-    pr = _capi._problem(q, k, v, bias, None, scale, seq_lens, seq_lens, cfg["causal"])
+    if packed:
+        lens = seq_lens.tolist()
+        q, k, v, do = (torch.cat([t[b, :n] for b, n in enumerate(lens)], 0) for t in (q, k, v, do))
+        cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32, device=q.device)
+        pr = _capi._problem(q, k, v, bias, None, scale, None, None, cfg["causal"],
+                            packed=(cu, cu, max(lens), max(lens)))
+    else:
+        pr = _capi._problem(q, k, v, bias, None, scale, seq_lens, seq_lens, cfg["causal"])
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     calls = {
@@ -391,13 +401,20 @@ def main():
         Pd = pairs(L, causal) * B * H
         dense_tf = 14 * D * Pd / (sum(kd.values()) * 1e-3) / 1e12
         padded_tf = 14 * D * P / (sum(kt.values()) * 1e-3) / 1e12
+        kp = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, args.steps),
+                          seq_lens=sl, packed=True)
+        packed_tf = 14 * D * P / (sum(kp.values()) * 1e-3) / 1e12
+        log("[bench] packed layout kernels (ms): " + ", ".join(f"{n}={t:.3f}" for n, t in kp.items()))
         padded_info = {
             "seq_lens": sl.tolist(),
             "valid_pair_fraction": round(P / Pd, 4),
             "padded_kernel_tflops": round(padded_tf, 2),
             "dense_kernel_tflops": round(dense_tf, 2),
             "padded_vs_dense": round(padded_tf / dense_tf, 4),
-            "note": "kernel sums (fwd + dQ + dK/dV) through the C ABI; padded counts valid pairs only",
+            "packed_kernel_tflops": round(packed_tf, 2),
+            "packed_vs_dense": round(packed_tf / dense_tf, 4),
+            "note": "kernel sums (fwd + dQ + dK/dV) through the C ABI; padded and packed (the same "
+                    "sequences as [rows, H, D] with cu_seqlens) count valid pairs only",
         }
         log(f"[bench] padded {padded_info}")
 

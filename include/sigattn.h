@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SIGATTN_ABI_VERSION 1
+#define SIGATTN_ABI_VERSION 2
 
 /* Element type of Q, K, V, dO and of every output. */
 enum sigattn_dtype {
@@ -48,7 +48,8 @@ enum sigattn_status {
   SIGATTN_ERR_STRIDE = -5,        /* negative stride */
   SIGATTN_ERR_DENSE_LENGTHS = -6, /* dense call (no seq_lens) with Tq != Tk */
   SIGATTN_ERR_ABI_VERSION = -7,   /* problem.abi_version != SIGATTN_ABI_VERSION */
-  SIGATTN_ERR_LAUNCH = -8         /* hipGetLastError() reported a failure */
+  SIGATTN_ERR_LAUNCH = -8,        /* hipGetLastError() reported a failure */
+  SIGATTN_ERR_LAYOUT = -9         /* seq_lens and cu_seqlens both set for one axis */
 };
 
 /*
@@ -72,6 +73,20 @@ typedef struct sigattn_problem {
   const int32_t *seq_lens_q; /* [B] int32 or NULL; NULL with seq_lens_k NULL = dense */
   const int32_t *seq_lens_k; /* [B] int32 or NULL */
   int32_t causal;         /* nonzero: key index <= query index (top-left) */
+  /*
+   * Packed variable-length layout (no counterpart in the reference's API; it
+   * is the layout its benchmark builds for flash_attn_varlen_func,
+   * benchmarks/benchmark_sigmoid.py:116-134).  When cu_seqlens_q is set,
+   * Q, O, dO and dQ are packed [rows_q, H, D] (q_stride_b is unused):
+   * sequence b is rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1, clamped to
+   * [0, rows_q] and to at most Tq rows (Tq = the longest sequence), and
+   * seq_lens_q must be NULL.  Likewise cu_seqlens_k / rows_k / Tk for K, V,
+   * dK, dV; score_mod is then packed [rows_k].  Outputs are written on the
+   * rows of the sequences only.
+   */
+  const int32_t *cu_seqlens_q; /* [B+1] int32 or NULL */
+  const int32_t *cu_seqlens_k; /* [B+1] int32 or NULL */
+  int64_t rows_q, rows_k;      /* packed row counts (used with cu_seqlens_*) */
 } sigattn_problem;
 
 /* ABI version compiled into the library. */
@@ -85,7 +100,8 @@ int sigattn_check(const sigattn_problem *p);
 
 /*
  * Forward: out[B, Tq, H, D] (q strides).  Rows at or past seq_lens_q[b] are
- * written as zeros.  `stream` is a hipStream_t (NULL = default stream).
+ * written as zeros (packed layout: only the sequences' rows are written).
+ * `stream` is a hipStream_t (NULL = default stream).
  */
 int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
 

@@ -71,6 +71,36 @@ def test_cpu_tensors_fail_loudly(fn):
         fn(q, q, q)
 
 
+def test_varlen_cpu_tensors_fail_loudly():
+    q = torch.randn(12, 2, 16)
+    cu = torch.tensor([0, 5, 12], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        ts.sigmoid_attention_varlen(q, q, q, cu, cu)
+
+
+# --- packed (THD) API validation
+
+def test_varlen_validation_errors():
+    q = torch.randn(12, 2, 16)
+    cu = torch.tensor([0, 5, 12], dtype=torch.int32)
+    with pytest.raises(ValueError, match="3D tensors"):
+        ts.sigmoid_attention_varlen(q[None], q[None], q[None], cu, cu)
+    with pytest.raises(ValueError, match="Number of heads mismatch"):
+        ts.sigmoid_attention_varlen(q, torch.randn(12, 3, 16), torch.randn(12, 3, 16), cu, cu)
+    with pytest.raises(ValueError, match="Head dimension mismatch"):
+        ts.sigmoid_attention_varlen(q, torch.randn(12, 2, 32), torch.randn(12, 2, 32), cu, cu)
+    with pytest.raises(ValueError, match="Key and value token counts must match"):
+        ts.sigmoid_attention_varlen(q, q, torch.randn(11, 2, 16), cu, cu)
+    with pytest.raises(ValueError, match=r"cu_seqlens_q must have shape \(B \+ 1,\)"):
+        ts.sigmoid_attention_varlen(q, q, q, cu[None], cu)
+    with pytest.raises(ValueError, match="same shape"):
+        ts.sigmoid_attention_varlen(q, q, q, cu, torch.tensor([0, 12], dtype=torch.int32))
+    with pytest.raises(ValueError, match=r"score_mod must have shape \(12,\)"):
+        ts.sigmoid_attention_varlen(q, q, q, cu, cu, score_mod=torch.zeros(2, 12))
+    with pytest.raises(ValueError, match="non-negative"):
+        ts.sigmoid_attention_varlen(q, q, q, cu, cu, max_seqlen_q=-1, max_seqlen_k=7)
+
+
 # --- operator boundary: names and schemas of the reference's ops
 
 @pytest.mark.parametrize("name,schema_args", [
@@ -80,6 +110,10 @@ def test_cpu_tensors_fail_loudly(fn):
                                  "sm_scale", "is_causal"]),
     ("sigmoid_attn_padded_bwd", ["Q", "K", "V", "dO", "seq_lens_k", "seq_lens_q", "bias", "score_mod",
                                  "sm_scale", "is_causal"]),
+    ("sigmoid_attn_varlen_fwd", ["Q", "K", "V", "cu_seqlens_k", "cu_seqlens_q", "max_seqlen_k", "max_seqlen_q",
+                                 "bias", "score_mod", "sm_scale", "is_causal"]),
+    ("sigmoid_attn_varlen_bwd", ["Q", "K", "V", "dO", "cu_seqlens_k", "cu_seqlens_q", "max_seqlen_k",
+                                 "max_seqlen_q", "bias", "score_mod", "sm_scale", "is_causal"]),
 ])
 def test_ops_registered_with_reference_schemas(name, schema_args):
     op = getattr(torch.ops.myops, name).default
@@ -106,6 +140,12 @@ def test_fake_tensor_shapes():
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
         o = torch.ops.myops.sigmoid_attention_fwd(q, q, q, bias, None, sc, True)
         assert o.shape == q.shape
+        qp, kp = torch.empty(50, 4, 64, dtype=torch.bfloat16), torch.empty(70, 4, 64, dtype=torch.bfloat16)
+        cu = torch.empty(3, dtype=torch.int32)
+        o = torch.ops.myops.sigmoid_attn_varlen_fwd(qp, kp, kp, cu, cu, 40, 30, bias, None, sc, True)
+        assert o.shape == qp.shape and o.dtype == qp.dtype
+        dq, dk, dv = torch.ops.myops.sigmoid_attn_varlen_bwd(qp, kp, kp, qp, cu, cu, 40, 30, bias, None, sc, False)
+        assert dq.shape == qp.shape and dk.shape == kp.shape and dv.shape == kp.shape
 
 
 def _trace_only_backend(graphs):

@@ -51,7 +51,7 @@ def test_abi_version_and_strerror():
     lib = _capi.load_library()
     assert lib.sigattn_abi_version() == _capi.ABI_VERSION
     assert lib.sigattn_strerror(0) == b"success"
-    for code in range(-8, 0):
+    for code in range(-9, 0):
         assert lib.sigattn_strerror(code) not in (b"", b"unknown sigattn status")
     assert lib.sigattn_strerror(-99) == b"unknown sigattn status"
 
@@ -82,6 +82,9 @@ def test_struct_layout_matches_header(tmp_path):
     (dict(Tq=1 << 40), -4),
     (dict(k_stride_t=-5), -5),
     (dict(Tk=8), -6),           # dense (no seq_lens) requires Tq == Tk
+    (dict(rows_q=-1, cu_seqlens_q=1 << 20), -4),
+    (dict(cu_seqlens_q=1 << 20, seq_lens_q=1 << 20), -9),   # one layout per axis
+    (dict(cu_seqlens_k=1 << 20, seq_lens_k=1 << 20), -9),
     (dict(bias=None), -1),
     (dict(scale=None), -1),
     (dict(q=None), -1),
@@ -111,6 +114,14 @@ def test_null_problem_and_null_outputs():
 def test_cross_attention_allowed_with_seq_lens():
     lib = _capi.load_library()
     p = _problem(Tk=8, seq_lens_k=1 << 20, seq_lens_q=1 << 20)
+    assert lib.sigattn_check(ctypes.byref(p)) == 0
+
+
+def test_packed_layout_allows_different_lengths():
+    lib = _capi.load_library()
+    p = _problem(Tk=8, cu_seqlens_q=1 << 20, cu_seqlens_k=1 << 20, rows_q=40, rows_k=20)
+    assert lib.sigattn_check(ctypes.byref(p)) == 0
+    p = _problem(Tk=8, cu_seqlens_q=1 << 20, seq_lens_k=1 << 20, rows_q=40)
     assert lib.sigattn_check(ctypes.byref(p)) == 0
 
 

@@ -1,0 +1,196 @@
+"""GPU parity tests for the packed variable-length path (sigmoid_attention_varlen
+-> myops::sigmoid_attn_varlen_fwd/bwd -> libsigattn.so with cu_seqlens set).
+
+The packed layout has no counterpart in the reference's operator API; its
+semantics are the padded operator's (sigmoid_triton_padded.py:853-1010) on the
+same sequences.  The kernels start their tiles at each sequence's first row in
+both layouts, so every valid output row must be bitwise equal to the padded
+path's, and the padded path is itself held to the float64 oracle."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import triton_sigmoid as ts
+from helpers import assert_close_to_oracle, oracle_fwd_bwd, randn
+from triton_sigmoid import _capi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _lengths(B, T, lo, g):
+    return torch.randint(int(lo * T), T + 1, (B,), generator=g, dtype=torch.int32)
+
+
+def _pack(x, lens):
+    """[B, T, H, D] -> [sum(lens), H, D] (valid rows only)."""
+    return torch.cat([x[b, :int(lens[b])] for b in range(x.shape[0])], 0)
+
+
+def _cu(lens):
+    return torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lens.long(), 0)]).to(torch.int32)
+
+
+def _case(B, Tq, Tk, H, D, dtype, seed, lo=0.3, same=True):
+    g = torch.Generator().manual_seed(seed)
+    q = randn((B, Tq, H, D), dtype, DEV, g)
+    k = randn((B, Tk, H, D), dtype, DEV, g)
+    v = randn((B, Tk, H, D), dtype, DEV, g)
+    do = randn((B, Tq, H, D), dtype, DEV, g)
+    sq = _lengths(B, Tq, lo, g)
+    sk = sq.clone() if (same and Tq == Tk) else _lengths(B, Tk, lo, g)
+    return q, k, v, do, sq, sk
+
+
+def _run_padded(q, k, v, do, sq, sk, causal, score_mod=None):
+    q, k, v = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk.to(DEV), seq_lens_q=sq.to(DEV), is_causal=causal,
+                                    score_mod=score_mod)
+    o.backward(do)
+    return o.detach(), q.grad, k.grad, v.grad
+
+
+def _run_varlen(q, k, v, do, sq, sk, causal, score_mod=None, max_given=True):
+    qp, kp, vp = (_pack(t, s).requires_grad_(True) for t, s in ((q, sq), (k, sk), (v, sk)))
+    dop = _pack(do, sq)
+    smp = None if score_mod is None else _pack(score_mod[..., None, None], sk)[:, 0, 0]
+    kw = dict(max_seqlen_q=int(sq.max()), max_seqlen_k=int(sk.max())) if max_given else {}
+    o = ts.sigmoid_attention_varlen(qp, kp, vp, _cu(sq).to(DEV), _cu(sk).to(DEV), is_causal=causal,
+                                    score_mod=smp, **kw)
+    o.backward(dop)
+    return o.detach(), qp.grad, kp.grad, vp.grad
+
+
+def _assert_equal_packed(padded, packed, sq, sk, what):
+    for name, P, V, lens in zip(("O", "dQ", "dK", "dV"), padded, packed, (sq, sq, sk, sk)):
+        want = _pack(P, lens)
+        assert V.shape == want.shape, (what, name)
+        assert torch.equal(V, want), f"{what} {name}: max diff {(V.float() - want.float()).abs().max().item()}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [16, 64, 128])
+@pytest.mark.parametrize("Tq,Tk", [(128, 128), (513, 513), (200, 77), (77, 300)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_equals_padded_bitwise(dtype, D, Tq, Tk, causal):
+    B, H = 3, 2
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=Tq * 7 + Tk + D)
+    _assert_equal_packed(_run_padded(q, k, v, do, sq, sk, causal),
+                         _run_varlen(q, k, v, do, sq, sk, causal), sq, sk, f"{dtype} D={D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_matches_oracle(dtype, causal):
+    B, T, H, D = 4, 300, 2, 64
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=11)
+    o, dq, dk, dv = _run_varlen(q, k, v, do, sq, sk, causal, max_given=False)
+    # The oracle sees the padded form with zeroed padding.
+    mask = lambda t, s: torch.stack([torch.where(torch.arange(T, device=DEV)[:, None, None] < s[b], t[b], 0)
+                                     for b in range(B)])
+    bias = (-torch.log(sk.float())).double().numpy()
+    want_o, (want_dq, want_dk, want_dv) = oracle_fwd_bwd(
+        mask(q, sq), mask(k, sk), mask(v, sk), mask(do, sq), scale=np.float32(1 / math.sqrt(D)), bias=bias,
+        seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    sel = lambda a, s: np.concatenate([a[b, :int(s[b])] for b in range(B)], 0)
+    assert_close_to_oracle(o, sel(want_o, sq), dtype, "O")
+    assert_close_to_oracle(dq, sel(want_dq, sq), dtype, "dQ")
+    assert_close_to_oracle(dk, sel(want_dk, sk), dtype, "dK")
+    assert_close_to_oracle(dv, sel(want_dv, sk), dtype, "dV")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_varlen_score_mod_equals_padded(D):
+    B, T, H = 3, 400, 2
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.bfloat16, seed=3)
+    g = torch.Generator().manual_seed(4)
+    sm = torch.randn((B, T), generator=g).to(DEV)
+    _assert_equal_packed(_run_padded(q, k, v, do, sq, sk, True, score_mod=sm),
+                         _run_varlen(q, k, v, do, sq, sk, True, score_mod=sm), sq, sk, "score_mod")
+
+
+def test_varlen_many_sequences_and_zero_lengths():
+    """B > 64 (grid in plain order) and empty sequences in the middle."""
+    B, T, H, D = 80, 96, 2, 64
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.float16, seed=5, lo=0.0)
+    sq[::7] = 0
+    sk.copy_(sq)
+    _assert_equal_packed(_run_padded(q, k, v, do, sq, sk, True),
+                         _run_varlen(q, k, v, do, sq, sk, True), sq, sk, "B=80")
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (32, torch.float32)])
+def test_packed_kernels_write_only_sequence_rows(D, dtype):
+    """Through the C ABI: rows outside every sequence keep their contents
+    (cu_seqlens ends before the last row), and sequences are computed as usual."""
+    lib = _capi.load_library()
+    H, rows = 2, 700
+    g = torch.Generator().manual_seed(9)
+    q, k, v, do = (randn((rows, H, D), dtype, DEV, g) for _ in range(4))
+    cu = torch.tensor([0, 250, 250, 611], dtype=torch.int32, device=DEV)   # rows 611.. are outside
+    bias = -torch.log(torch.tensor([250.0, 0.0, 361.0], device=DEV))   # as the API computes it
+    scale = torch.tensor(1 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, True, packed=(cu, cu, 361, 361))
+    out, dq, dk, dv = (torch.full_like(q, float("nan")) for _ in range(4))
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream) == 0
+    assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                           stream) == 0
+    torch.cuda.synchronize()
+    for t in (out, dq, dk, dv):
+        assert torch.all(torch.isnan(t[611:]))
+        assert torch.all(torch.isfinite(t[:611]))
+    want = ts.sigmoid_attention_varlen(q[:611], k[:611], v[:611], cu, cu, 361, 361, is_causal=True)
+    assert torch.equal(out[:611], want)
+
+
+def test_varlen_empty_batch_and_validation():
+    H, D = 2, 64
+    q = torch.zeros((0, H, D), dtype=torch.bfloat16, device=DEV)
+    cu = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert ts.sigmoid_attention_varlen(q, q, q, cu, cu).shape == (0, H, D)
+    x = torch.zeros((10, H, D), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="3D tensors"):
+        ts.sigmoid_attention_varlen(x[None], x[None], x[None], cu, cu)
+    with pytest.raises(ValueError, match="same shape"):
+        ts.sigmoid_attention_varlen(x, x, x, torch.tensor([0, 10], device=DEV),
+                                    torch.tensor([0, 5, 10], device=DEV))
+    with pytest.raises(ValueError, match="score_mod must have shape"):
+        ts.sigmoid_attention_varlen(x, x, x, cu, cu, score_mod=torch.zeros(3, device=DEV))
+
+
+def test_varlen_under_torch_compile():
+    B, T, H, D = 3, 256, 4, 64
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.bfloat16, seed=21)
+    qp, kp, vp = _pack(q, sq), _pack(k, sk), _pack(v, sk)
+    cq, ck = _cu(sq).to(DEV), _cu(sk).to(DEV)
+    mq, mk = int(sq.max()), int(sk.max())
+    torch._dynamo.reset()
+    fn = lambda a, b, c, **kw: ts.sigmoid_attention_varlen(a, b, c, cq, ck, mq, mk, is_causal=True, **kw)
+    compiled = torch.compile(fn, fullgraph=True)
+    le = [t.clone().requires_grad_(True) for t in (qp, kp, vp)]
+    lc = [t.clone().requires_grad_(True) for t in (qp, kp, vp)]
+    oe, oc = fn(*le), compiled(*lc)
+    # Compiled, the default bias -log(len) comes from Inductor's own kernel and
+    # may differ from eager ATen by an fp32 ulp (as for the padded op).
+    tol = 2 * 7e-3
+    torch.testing.assert_close(oe, oc, atol=tol, rtol=0)
+    dop = _pack(do, sq)
+    oe.backward(dop)
+    oc.backward(dop)
+    for a, b in zip(le, lc):
+        torch.testing.assert_close(a.grad, b.grad, atol=tol, rtol=0)
+    # With an explicit bias both run identical kernels: bitwise equal.
+    assert torch.equal(compiled(qp, kp, vp, sigmoid_bias=-3.0), fn(qp, kp, vp, sigmoid_bias=-3.0))
+
+
+def test_varlen_c5_shape_equals_padded():
+    """BASELINE configs[4] (bf16 B=4 Lmax=8192 H=12 D=64, non-causal) packed."""
+    B, T, H, D = 4, 8192, 12, 64
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.bfloat16, seed=1, lo=0.125)
+    _assert_equal_packed(_run_padded(q, k, v, do, sq, sk, False),
+                         _run_varlen(q, k, v, do, sq, sk, False), sq, sk, "c5 shape")

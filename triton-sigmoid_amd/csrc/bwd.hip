@@ -42,9 +42,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? 2 * BN : 4];
 
   int b, h, qb;
-  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, true)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, p.seq_k, p.Tk);
+  if (p.ragged() && p.B <= 64) {
+    const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
+    const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb = it.blk;
   } else {
     const int BH = p.B * p.H;
@@ -53,15 +55,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }
-  const int Lq = clamp_len(p.seq_q, b, p.Tq);
-  const int Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b);
+  const int Lk = p.len_k(b);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int q0 = qb * BM, qw = q0 + w * 32, my_q = qw + l32;
 
-  const int64_t qoff = (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const int64_t koff = (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
+  const int64_t qoff = p.q_base(b, h);
+  const int64_t koff = p.k_base(b, h);
   const uint16_t *Qb = (const uint16_t *)p.q + qoff;
   const uint16_t *dOb = (const uint16_t *)p.dout + qoff;
   const uint16_t *Kb = (const uint16_t *)p.k + koff;
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   auto load_c = [&](int n0) SIGATTN_INLINE {
     if (SCOREMOD && tid < BN) {
       const int key = n0 + tid;
-      creg = key < Lk ? -(bias + p.score_mod[(int64_t)b * p.Tk + key]) * kLog2e : 0.0f;
+      creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
     }
   };
   auto issue = [&](int st, int n0) SIGATTN_INLINE {
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     if (it + 1 < ntiles) iteration(it + 1, std::integral_constant<int, 1>{});
   }
 
-  if (my_q < p.Tq) {
+  if (my_q < p.q_rows_out(Lq)) {
     uint16_t *row = dQb + (int64_t)my_q * p.sq_t;
     const bool valid = my_q < Lq;
 #pragma unroll
@@ -245,9 +247,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];
 
   int b, h, kblk;
-  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_k, p.Tk, BN, p.nblk, false)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_k, p.Tk, BN, p.nblk, p.seq_q, p.Tq);
+  if (p.ragged() && p.B <= 64) {
+    const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
+    const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lk, BN, p.nblk, false)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lk, BN, p.nblk, lq);
     b = it.b, h = it.h, kblk = it.blk;
   } else {
     const int BH = p.B * p.H;
@@ -255,16 +259,16 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     kblk = blockIdx.x / BH;  // causal: low key blocks carry the most work and come first
     b = bh / p.H, h = bh % p.H;
   }
-  const int Lq = clamp_len(p.seq_q, b, p.Tq);
-  const int Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b);
+  const int Lk = p.len_k(b);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int k0 = kblk * BN, kw = k0 + w * 32, my_k = kw + l32;
 
-  const int64_t qoff = (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const int64_t koff = (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
+  const int64_t qoff = p.q_base(b, h);
+  const int64_t koff = p.k_base(b, h);
   const uint16_t *Qb = (const uint16_t *)p.q + qoff;
   const uint16_t *dOb = (const uint16_t *)p.dout + qoff;
   const uint16_t *Kb = (const uint16_t *)p.k + koff;
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   const float nsl = -scale * kLog2e;
   const bool kok = my_k < Lk;
   float nc = -bias * kLog2e;
-  if (SCOREMOD) nc = kok ? -(bias + p.score_mod[(int64_t)b * p.Tk + my_k]) * kLog2e : 0.0f;
+  if (SCOREMOD) nc = kok ? -(bias + p.score_mod[p.mod_base(b) + my_k]) * kLog2e : 0.0f;
 
   u32x4 kf[NKS], vf[NKS];
   {
@@ -481,7 +485,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
   }
 
-  if (my_k < p.Tk) {
+  if (my_k < p.k_rows_out(Lk)) {
     uint16_t *kr = dKb + (int64_t)my_k * p.sk_t;
     uint16_t *vr = dVb + (int64_t)my_k * p.sk_t;
 #pragma unroll

@@ -33,6 +33,10 @@ KParams make_params(const sigattn_problem *p) {
   k.score_mod = p->score_mod;
   k.seq_q = p->seq_lens_q;
   k.seq_k = p->seq_lens_k;
+  k.cu_q = p->cu_seqlens_q;
+  k.cu_k = p->cu_seqlens_k;
+  k.rows_q = p->rows_q;
+  k.rows_k = p->rows_k;
   k.sq_b = p->q_stride_b;
   k.sq_t = p->q_stride_t;
   k.sq_h = p->q_stride_h;
@@ -46,11 +50,19 @@ KParams make_params(const sigattn_problem *p) {
   return k;
 }
 
+// T rows of `stride` 16-bit elements span less than 2^31 bytes.
+bool rows_fit_2g(int64_t T, int64_t stride) {
+  return stride == 0 || T <= (((int64_t)1 << 30) - 1) / stride;
+}
+
 // True when the MFMA kernels can take the problem: 16-bit elements, D of 64
-// or 128, and every row start 16-byte aligned.
+// or 128, every row start 16-byte aligned, and every row of a sequence within
+// 2^31 bytes of the sequence's first row (the tile copies address rows with a
+// 32-bit byte offset from that row).
 bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
   if (p->dtype == SIGATTN_F32) return false;
   if (p->D != 64 && p->D != 128) return false;
+  if (!rows_fit_2g(p->Tq, p->q_stride_t) || !rows_fit_2g(p->Tk, p->k_stride_t)) return false;
   const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
                               p->k_stride_b, p->k_stride_t, p->k_stride_h};
   for (int64_t s : strides)
@@ -82,6 +94,8 @@ const char *sigattn_strerror(int status) {
       return "dense attention (no seq_lens) requires the same sequence length for Q and K";
     case SIGATTN_ERR_ABI_VERSION: return "sigattn_problem.abi_version does not match the library";
     case SIGATTN_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SIGATTN_ERR_LAYOUT:
+      return "seq_lens and cu_seqlens cannot both be given for the same sequence axis";
     default: return "unknown sigattn status";
   }
 }
@@ -93,6 +107,10 @@ int sigattn_check(const sigattn_problem *p) {
     return SIGATTN_ERR_DTYPE;
   if (!is_pow2_head_dim(p->D)) return SIGATTN_ERR_HEAD_DIM;
   if (p->B < 0 || p->Tq < 0 || p->Tk < 0 || p->H < 0) return SIGATTN_ERR_SHAPE;
+  if (p->rows_q < 0 || p->rows_k < 0) return SIGATTN_ERR_SHAPE;
+  if ((p->cu_seqlens_q != nullptr && p->seq_lens_q != nullptr) ||
+      (p->cu_seqlens_k != nullptr && p->seq_lens_k != nullptr))
+    return SIGATTN_ERR_LAYOUT;
   if (p->Tq > (INT_MAX / 2) || p->Tk > (INT_MAX / 2) || p->B > INT_MAX || p->H > INT_MAX)
     return SIGATTN_ERR_SHAPE;
   // Largest grid any kernel launches: ceil(T / 64) row blocks per (b, h).
@@ -102,7 +120,8 @@ int sigattn_check(const sigattn_problem *p) {
                               p->k_stride_b, p->k_stride_t, p->k_stride_h};
   for (int64_t s : strides)
     if (s < 0) return SIGATTN_ERR_STRIDE;
-  if (p->seq_lens_q == nullptr && p->seq_lens_k == nullptr && p->Tq != p->Tk)
+  if (p->seq_lens_q == nullptr && p->seq_lens_k == nullptr && p->cu_seqlens_q == nullptr &&
+      p->cu_seqlens_k == nullptr && p->Tq != p->Tk)
     return SIGATTN_ERR_DENSE_LENGTHS;
   if (p->B == 0 || p->H == 0) return SIGATTN_OK;
   if (p->bias == nullptr || p->scale == nullptr) return SIGATTN_ERR_NULL_ARG;

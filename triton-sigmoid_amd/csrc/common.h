@@ -36,26 +36,82 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // log2(e): sigmoid(x) = 1 / (1 + 2^(-x * log2(e))).
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Kernel parameters (passed by value).  Strides are in elements.
-struct KParams {
-  const void *q, *k, *v, *dout;
-  void *out, *dq, *dk, *dv;
-  const float *bias;       // [B]
-  const float *scale;      // 0-d
-  const float *score_mod;  // [B, Tk] fp32 contiguous or nullptr
-  const int32_t *seq_q;    // [B] or nullptr (= Tq)
-  const int32_t *seq_k;    // [B] or nullptr (= Tk)
-  int64_t sq_b, sq_t, sq_h;  // Q / O / dO / dQ
-  int64_t sk_b, sk_t, sk_h;  // K / V / dK / dV
-  int B, H, Tq, Tk;
-  int nblk;  // number of row blocks along the stationary sequence axis
-};
-
 __device__ __forceinline__ int clamp_len(const int32_t *lens, int b, int T) {
   if (lens == nullptr) return T;
   int L = lens[b];
   return L < 0 ? 0 : (L > T ? T : L);
 }
+
+// First row of sequence b in a packed [rows, H, D] tensor: cu[b] clamped to
+// [0, rows].
+__device__ __forceinline__ int64_t packed_first(const int32_t *cu, int64_t rows, int b) {
+  const int64_t s = cu[b];
+  return s < 0 ? 0 : (s > rows ? rows : s);
+}
+
+// Rows of sequence b in a packed tensor: cu[b+1] - cu[b] after both are
+// clamped to [0, rows] (so first + length <= rows), at most T.
+__device__ __forceinline__ int packed_len(const int32_t *cu, int64_t rows, int b, int T) {
+  const int64_t s = packed_first(cu, rows, b);
+  int64_t e = cu[b + 1];
+  e = e < s ? s : (e > rows ? rows : e);
+  return (int)(e - s < T ? e - s : T);
+}
+
+// Kernel parameters (passed by value).  Strides are in elements.
+//
+// Each sequence axis (queries, keys) has one of three layouts:
+//   * dense: batch b holds T rows at b * stride_b;
+//   * padded (seq_* set): the first seq_*[b] of those T rows are valid;
+//   * packed (cu_* set): tensors are [rows, H, D] and batch b holds rows
+//     cu_*[b] .. cu_*[b+1]-1 (at most T = the longest sequence).
+// Padded outputs write zeros to the invalid rows of each batch; packed
+// outputs write exactly the rows of each sequence and nothing else.
+struct KParams {
+  const void *q, *k, *v, *dout;
+  void *out, *dq, *dk, *dv;
+  const float *bias;       // [B]
+  const float *scale;      // 0-d
+  const float *score_mod;  // [B, Tk] (packed keys: [rows_k]) fp32 contiguous or nullptr
+  const int32_t *seq_q;    // [B] or nullptr (= Tq)
+  const int32_t *seq_k;    // [B] or nullptr (= Tk)
+  const int32_t *cu_q;     // [B+1] packed query offsets or nullptr
+  const int32_t *cu_k;     // [B+1] packed key offsets or nullptr
+  int64_t rows_q, rows_k;  // packed row counts (with cu_q / cu_k)
+  int64_t sq_b, sq_t, sq_h;  // Q / O / dO / dQ
+  int64_t sk_b, sk_t, sk_h;  // K / V / dK / dV
+  int B, H, Tq, Tk;
+  int nblk;  // number of row blocks along the stationary sequence axis
+
+  // Valid query / key rows of batch b.
+  __device__ __forceinline__ int len_q(int b) const {
+    return cu_q != nullptr ? packed_len(cu_q, rows_q, b, Tq) : clamp_len(seq_q, b, Tq);
+  }
+  __device__ __forceinline__ int len_k(int b) const {
+    return cu_k != nullptr ? packed_len(cu_k, rows_k, b, Tk) : clamp_len(seq_k, b, Tk);
+  }
+  // Element offset of row 0 of (b, h) in the Q-shaped / K-shaped tensors.
+  __device__ __forceinline__ int64_t q_base(int b, int h) const {
+    const int64_t r = cu_q != nullptr ? packed_first(cu_q, rows_q, b) * sq_t : (int64_t)b * sq_b;
+    return r + (int64_t)h * sq_h;
+  }
+  __device__ __forceinline__ int64_t k_base(int b, int h) const {
+    const int64_t r = cu_k != nullptr ? packed_first(cu_k, rows_k, b) * sk_t : (int64_t)b * sk_b;
+    return r + (int64_t)h * sk_h;
+  }
+  // score_mod entry of key 0 of batch b.
+  __device__ __forceinline__ int64_t mod_base(int b) const {
+    return cu_k != nullptr ? packed_first(cu_k, rows_k, b) : (int64_t)b * Tk;
+  }
+  // Rows of batch b an output kernel writes (zeros past the valid length
+  // in the padded layout; only the sequence itself in the packed layout).
+  __device__ __forceinline__ int q_rows_out(int Lq) const { return cu_q != nullptr ? Lq : Tq; }
+  __device__ __forceinline__ int k_rows_out(int Lk) const { return cu_k != nullptr ? Lk : Tk; }
+  // Batches differ in length (the work order then follows the lengths).
+  __device__ __forceinline__ bool ragged() const {
+    return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Work-item order.  A kernel's grid covers (row block, batch, head) items of
@@ -72,7 +128,8 @@ __device__ __forceinline__ int clamp_len(const int32_t *lens, int b, int T) {
 //     grows with the query block, or shrinks with the key block), the batches
 //     valid at a level in index order, heads fastest.
 // Padding items (row block past a batch's length) come after all valid items,
-// batch by batch; their workgroups only write the zero rows.  Every lane of
+// batch by batch; their workgroups only write the zero rows (padded layout)
+// or nothing (packed layout).  Every lane of
 // every wave computes the same answer (lane j holds batch j), so B is limited
 // to 64; callers keep the dense order beyond that.
 struct WorkItem {
@@ -80,10 +137,11 @@ struct WorkItem {
 };
 
 struct WorkOrder {
-  // Row blocks of batch `lane` (0 for lanes past B).
-  static __device__ __forceinline__ int row_blocks(const int32_t *rows, int T, int RB, int B, int lane) {
+  // Row blocks of batch `lane` (0 for lanes past B); rows(b) = valid rows.
+  template <class Len>
+  static __device__ __forceinline__ int row_blocks(Len rows, int RB, int B, int lane) {
     if (lane >= B) return 0;
-    return (clamp_len(rows, lane, T) + RB - 1) / RB;
+    return (rows(lane) + RB - 1) / RB;
   }
   static __device__ __forceinline__ int kth_set_bit(uint64_t m, int k) {
     for (int t = 0; t < k; ++t) m &= m - 1;
@@ -101,11 +159,12 @@ struct WorkOrder {
     const int r = j - __builtin_amdgcn_readlane(start, b);
     return WorkItem{b, r % H, __builtin_amdgcn_readlane(nv, b) + r / H};
   }
-  static __device__ __forceinline__ WorkItem by_stream(int id, int B, int H, const int32_t *rows, int Trows,
-                                                       int RB, int nlev, const int32_t *stream, int Tstream) {
+  template <class RowLen, class StreamLen>
+  static __device__ __forceinline__ WorkItem by_stream(int id, int B, int H, RowLen rows, int RB, int nlev,
+                                                       StreamLen stream) {
     const int lane = __lane_id();
-    const int nv = row_blocks(rows, Trows, RB, B, lane);
-    const int key = lane < B ? clamp_len(stream, lane, Tstream) : -1;
+    const int nv = row_blocks(rows, RB, B, lane);
+    const int key = lane < B ? stream(lane) : -1;
     const int cnt = nv * H;
     int rank = 0, total = 0;
     for (int k = 0; k < B; ++k) {
@@ -124,10 +183,11 @@ struct WorkOrder {
     const int r = id - __builtin_amdgcn_readlane(start, b);
     return WorkItem{b, r % H, r / H};
   }
-  static __device__ __forceinline__ WorkItem by_level(int id, int B, int H, const int32_t *rows, int Trows,
-                                                      int RB, int nlev, bool descending) {
+  template <class RowLen>
+  static __device__ __forceinline__ WorkItem by_level(int id, int B, int H, RowLen rows, int RB, int nlev,
+                                                      bool descending) {
     const int lane = __lane_id();
-    const int nv = row_blocks(rows, Trows, RB, B, lane);
+    const int nv = row_blocks(rows, RB, B, lane);
     int base = 0;
     for (int t = 0; t < nlev; ++t) {
       const int lev = descending ? nlev - 1 - t : t;

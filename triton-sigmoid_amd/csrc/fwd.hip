@@ -52,9 +52,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? NST * BN : 4];
 
   int b, h, qb;
-  if ((p.seq_q != nullptr || p.seq_k != nullptr) && p.B <= 64) {
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, true)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, p.seq_q, p.Tq, BM, p.nblk, p.seq_k, p.Tk);
+  if (p.ragged() && p.B <= 64) {
+    const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
+    const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb = it.blk;
   } else {
     const int BH = p.B * p.H;
@@ -64,8 +66,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
     b = bh / p.H, h = bh % p.H;
   }
 
-  const int Lq = clamp_len(p.seq_q, b, p.Tq);
-  const int Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b);
+  const int Lk = p.len_k(b);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -78,10 +80,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   const int qw = q0 + slot * QW;    // this wave's first query
   const int myq0 = qw + l32;        // this lane's query in column block 0 (block c: +32c)
 
-  const uint16_t *Qb = (const uint16_t *)p.q + (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const uint16_t *Kb = (const uint16_t *)p.k + (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
-  const uint16_t *Vb = (const uint16_t *)p.v + (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
-  uint16_t *Ob = (uint16_t *)p.out + (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
+  const int64_t qoff = p.q_base(b, h), koff = p.k_base(b, h);
+  const uint16_t *Qb = (const uint16_t *)p.q + qoff;
+  const uint16_t *Kb = (const uint16_t *)p.k + koff;
+  const uint16_t *Vb = (const uint16_t *)p.v + koff;
+  uint16_t *Ob = (uint16_t *)p.out + qoff;
 
   int nend = Lk;
   if (CAUSAL) nend = min(nend, min(q0 + BM, Lq));
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   auto load_c = [&](int n0) SIGATTN_INLINE {
     if (SCOREMOD && tid < BN) {
       const int key = n0 + tid;
-      creg = key < Lk ? -(bias + p.score_mod[(int64_t)b * p.Tk + key]) * kLog2e : 0.0f;
+      creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
     }
   };
   auto issue = [&](int st, int t) SIGATTN_INLINE {
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
 #pragma unroll
   for (int c = 0; c < NCB; ++c) {
     const int q = myq0 + 32 * c;
-    if (q < p.Tq) {
+    if (q < p.q_rows_out(Lq)) {
       uint16_t *orow = Ob + (int64_t)q * p.sq_t;
       const bool valid = q < Lq;
 #pragma unroll

@@ -37,10 +37,10 @@ __global__ __launch_bounds__(GB) void fwd_generic_kernel(const KParams p) {
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH, qb = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int Lq = clamp_len(p.seq_q, b, p.Tq), Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b), Lk = p.len_k(b);
   const int q = qb * GB + threadIdx.x;
-  const int64_t qbase = (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const int64_t kbase = (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
+  const int64_t qbase = p.q_base(b, h);
+  const int64_t kbase = p.k_base(b, h);
   const float scale = *p.scale, bias = p.bias[b];
 
   float qv[D], acc[D];
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(GB) void fwd_generic_kernel(const KParams p) {
     }
     if (threadIdx.x < GT) {
       const int key = n0 + threadIdx.x;
-      sC[threadIdx.x] = (p.score_mod && key < Lk) ? p.score_mod[(int64_t)b * p.Tk + key] : 0.0f;
+      sC[threadIdx.x] = (p.score_mod && key < Lk) ? p.score_mod[p.mod_base(b) + key] : 0.0f;
     }
     __syncthreads();
     const int jn = min(GT, nend - n0);
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(GB) void fwd_generic_kernel(const KParams p) {
     }
     __syncthreads();
   }
-  if (q < p.Tq) {
+  if (q < p.q_rows_out(Lq)) {
 #pragma unroll
     for (int d = 0; d < D; ++d) st<T>(p.out, qbase + (int64_t)q * p.sq_t + d, qok ? acc[d] : 0.0f);
   }
@@ -93,10 +93,10 @@ __global__ __launch_bounds__(GB) void dq_generic_kernel(const KParams p) {
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH, qb = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int Lq = clamp_len(p.seq_q, b, p.Tq), Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b), Lk = p.len_k(b);
   const int q = qb * GB + threadIdx.x;
-  const int64_t qbase = (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const int64_t kbase = (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
+  const int64_t qbase = p.q_base(b, h);
+  const int64_t kbase = p.k_base(b, h);
   const float scale = *p.scale, bias = p.bias[b];
 
   float qv[D], dov[D], acc[D];
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(GB) void dq_generic_kernel(const KParams p) {
     }
     if (threadIdx.x < GT) {
       const int key = n0 + threadIdx.x;
-      sC[threadIdx.x] = (p.score_mod && key < Lk) ? p.score_mod[(int64_t)b * p.Tk + key] : 0.0f;
+      sC[threadIdx.x] = (p.score_mod && key < Lk) ? p.score_mod[p.mod_base(b) + key] : 0.0f;
     }
     __syncthreads();
     const int jn = min(GT, nend - n0);
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(GB) void dq_generic_kernel(const KParams p) {
     }
     __syncthreads();
   }
-  if (q < p.Tq) {
+  if (q < p.q_rows_out(Lq)) {
 #pragma unroll
     for (int d = 0; d < D; ++d)
       st<T>(p.dq, qbase + (int64_t)q * p.sq_t + d, qok ? acc[d] * scale : 0.0f);
@@ -155,13 +155,13 @@ __global__ __launch_bounds__(GB) void dkdv_generic_kernel(const KParams p) {
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH, kb = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int Lq = clamp_len(p.seq_q, b, p.Tq), Lk = clamp_len(p.seq_k, b, p.Tk);
+  const int Lq = p.len_q(b), Lk = p.len_k(b);
   const int key = kb * GB + threadIdx.x;
-  const int64_t qbase = (int64_t)b * p.sq_b + (int64_t)h * p.sq_h;
-  const int64_t kbase = (int64_t)b * p.sk_b + (int64_t)h * p.sk_h;
+  const int64_t qbase = p.q_base(b, h);
+  const int64_t kbase = p.k_base(b, h);
   const float scale = *p.scale, bias = p.bias[b];
   const bool kok = key < Lk;
-  const float c = bias + ((p.score_mod && kok) ? p.score_mod[(int64_t)b * p.Tk + key] : 0.0f);
+  const float c = bias + ((p.score_mod && kok) ? p.score_mod[p.mod_base(b) + key] : 0.0f);
 
   float kv[D], vv[D], dk[D], dv[D];
 #pragma unroll
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(GB) void dkdv_generic_kernel(const KParams p) {
     }
     __syncthreads();
   }
-  if (key < p.Tk) {
+  if (key < p.k_rows_out(Lk)) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       st<T>(p.dk, kbase + (int64_t)key * p.sk_t + d, kok ? dk[d] * scale : 0.0f);

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsigattn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F16, BF16, F32 = 0, 1, 2
 _DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
@@ -50,6 +50,10 @@ class SigattnProblem(ctypes.Structure):
         ("seq_lens_q", _c_vp),
         ("seq_lens_k", _c_vp),
         ("causal", _c_i32),
+        ("cu_seqlens_q", _c_vp),
+        ("cu_seqlens_k", _c_vp),
+        ("rows_q", _c_i64),
+        ("rows_k", _c_i64),
     ]
 
 
@@ -120,11 +124,22 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) -> SigattnProblem:
-    B, Tq, H, D = Q.shape
-    Tk = K.shape[1]
-    qs, ks = Q.stride(), K.stride()
+def _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal,
+             packed=None) -> SigattnProblem:
+    """One sigattn_problem.  `packed` = (cu_seqlens_q, cu_seqlens_k,
+    max_seqlen_q, max_seqlen_k) for [rows, H, D] tensors, else [B, T, H, D]."""
     pr = SigattnProblem()
+    if packed is None:
+        B, Tq, H, D = Q.shape
+        Tk = K.shape[1]
+        qs, ks = Q.stride(), K.stride()
+    else:
+        cu_q, cu_k, Tq, Tk = packed
+        B = cu_q.numel() - 1
+        H, D = Q.shape[1], Q.shape[2]
+        qs, ks = (0,) + Q.stride(), (0,) + K.stride()
+        pr.cu_seqlens_q, pr.cu_seqlens_k = _ptr(cu_q), _ptr(cu_k)
+        pr.rows_q, pr.rows_k = Q.shape[0], K.shape[0]
     pr.abi_version = ABI_VERSION
     pr.dtype = _DTYPE_CODE[Q.dtype]
     pr.B, pr.Tq, pr.Tk, pr.H, pr.D = B, Tq, Tk, H, D
@@ -194,6 +209,60 @@ def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, cau
     if dQ.numel() == 0 and dK.numel() == 0:
         return dQ, dK, dV
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream(Q.device).cuda_stream
+        rc = lib.sigattn_bwd(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), stream)
+        _raise(rc, "sigattn_bwd")
+    return dQ, dK, dV
+
+
+def _prepare_packed(cu_seqlens_q, cu_seqlens_k, dev):
+    cu_q = cu_seqlens_q.to(device=dev, dtype=torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(device=dev, dtype=torch.int32).contiguous()
+    if cu_q.shape != cu_k.shape or cu_q.dim() != 1 or cu_q.numel() < 1:
+        raise RuntimeError(f"cu_seqlens_q {tuple(cu_q.shape)} and cu_seqlens_k {tuple(cu_k.shape)} "
+                           "must both be [B + 1]")
+    return cu_q, cu_k
+
+
+def _packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k):
+    # An axis with no rows has no valid positions whatever max_seqlen says.
+    Tq = int(max_seqlen_q) if Q.shape[0] > 0 else 0
+    Tk = int(max_seqlen_k) if K.shape[0] > 0 else 0
+    return cu_q, cu_k, Tq, Tk
+
+
+def forward_packed(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, bias, score_mod,
+                   sm_scale, causal) -> torch.Tensor:
+    """Forward for packed [rows, H, D] tensors via sigattn_fwd (cu_seqlens set)."""
+    lib = load_library()
+    Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
+    cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
+    out = torch.empty_like(Q)
+    if out.numel() == 0 or cu_q.numel() == 1:
+        return out
+    pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
+                  packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream(Q.device).cuda_stream
+        _raise(lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream), "sigattn_fwd")
+    return out
+
+
+def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, bias, score_mod,
+                    sm_scale, causal):
+    """(dQ, dK, dV) for packed [rows, H, D] tensors via sigattn_bwd."""
+    lib = load_library()
+    Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
+    cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
+    dO = dO.to(dtype=Q.dtype).contiguous()
+    if dO.shape != Q.shape:
+        raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
+    dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    if (dQ.numel() == 0 and dK.numel() == 0) or cu_q.numel() == 1:
+        return dQ, dK, dV
+    pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
+                  packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
     with torch.cuda.device(Q.device):
         stream = torch.cuda.current_stream(Q.device).cuda_stream
         rc = lib.sigattn_bwd(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), stream)
