@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT / "triton-sigmoid_amd"))
 sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_TBPS = 8.0        # MI355X HBM3E
 METRIC = "fwd & fwd+bwd TFLOPS + % of fp16 MFMA peak, dense/padded L=4096 D=128"
 
 CONFIGS = {
@@ -301,6 +302,75 @@ def sweep():
     return rows
 
 
+# Decode shapes for the split-KV forward (bench.py --decode): bf16, Tq new
+# queries per sequence against a KV cache, non-causal; "lo" = cache lengths
+# ~ U[lo, Tk] per sequence (seeded), else every cache is Tk long.
+DECODE_CONFIGS = [
+    dict(B=16, H=32, D=128, Tq=1, Tk=8192),
+    dict(B=16, H=32, D=128, Tq=1, Tk=8192, lo=1024),
+    dict(B=1, H=32, D=128, Tq=1, Tk=131072),
+    dict(B=32, H=32, D=64, Tq=4, Tk=4096),
+    dict(B=8, H=16, D=128, Tq=32, Tk=16384),
+]
+
+
+def decode_bench(iters: int = 20):
+    """Split-KV forward at decode shapes through the C ABI: average kernel time
+    (the chunk kernel and the partial sum) with the workspace the library asks
+    for, and with none (one chunk per (batch, head)), on torch's current stream
+    between HIP events.  The kernel is HBM-bound: its algorithmic traffic is
+    K and V of the valid cache (2 * D * 2 bytes per key, batch and head) plus
+    Q and O."""
+    import ctypes
+    import torch
+    from triton_sigmoid import _capi
+    lib = _capi.load_library()
+    dev = torch.device("cuda", 0)
+    rows = []
+    for cfg in DECODE_CONFIGS:
+        B, H, D, Tq, Tk = cfg["B"], cfg["H"], cfg["D"], cfg["Tq"], cfg["Tk"]
+        g = torch.Generator(device=dev).manual_seed(B * Tk + D)
+        q = torch.randn((B, Tq, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn((B, Tk, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn((B, Tk, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        gc = torch.Generator().manual_seed(Tk + B)
+        lens = (torch.randint(cfg["lo"], Tk + 1, (B,), generator=gc, dtype=torch.int32) if "lo" in cfg
+                else torch.full((B,), Tk, dtype=torch.int32))
+        sk = lens.to(dev)
+        sq = torch.full((B,), Tq, dtype=torch.int32, device=dev)
+        bias = -torch.log(sk.float())
+        scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=dev)
+        pr = _capi._problem(q, k, v, bias, None, scale, sq, sk, False)
+        out = torch.empty_like(q)
+        nbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream().cuda_stream
+        kv_keys = int(lens.sum())
+        traffic = 2 * D * 2 * kv_keys * H + 2 * B * Tq * H * D * 2
+        flops = 4 * D * Tq * kv_keys * H
+        row = dict(cfg, workspace_bytes=nbytes)
+        for name, wptr, wbytes in (("split", ws.data_ptr() if nbytes else None, nbytes), ("one_chunk", None, 0)):
+            call = lambda: lib.sigattn_fwd_ws(ctypes.byref(pr), out.data_ptr(), wptr, wbytes, stream)
+            for _ in range(3):
+                assert call() == 0
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                call()
+            e.record()
+            e.synchronize()
+            ms = s.elapsed_time(e) / iters
+            row[name] = dict(ms=round(ms, 4), gbps=round(traffic / ms / 1e6, 1),
+                             hbm_frac=round(traffic / ms / 1e6 / (HBM_PEAK_TBPS * 1e3), 4),
+                             tflops=round(flops / ms / 1e9, 1))
+        rows.append(row)
+        log(f"[decode] {cfg}: split {row['split']} | one chunk {row['one_chunk']}")
+        del q, k, v, out, ws
+        torch.cuda.empty_cache()
+    return rows
+
+
 def workload_name(name, cfg) -> str:
     shape = f"B={cfg['B']} L={cfg['L']} H={cfg['H']} D={cfg['D']} {cfg['dtype']} causal={cfg['causal']}"
     if cfg.get("padded"):
@@ -323,9 +393,16 @@ def main():
                     help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference benchmark's L/D/padding grid, beside its published H100 chart")
+    ap.add_argument("--decode", action="store_true",
+                    help="split-KV forward at decode shapes (HBM GB/s)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.decode:
+        rows = decode_bench()
+        print(json.dumps({"metric": "split-KV decode forward: HBM GB/s of K, V, Q, O", "unit": "GB/s",
+                          "peak_tbps": HBM_PEAK_TBPS, "rows": rows}), flush=True)
         return
     if args.sweep:
         rows = sweep()

@@ -49,7 +49,8 @@ enum sigattn_status {
   SIGATTN_ERR_DENSE_LENGTHS = -6, /* dense call (no seq_lens) with Tq != Tk */
   SIGATTN_ERR_ABI_VERSION = -7,   /* problem.abi_version != SIGATTN_ABI_VERSION */
   SIGATTN_ERR_LAUNCH = -8,        /* hipGetLastError() reported a failure */
-  SIGATTN_ERR_LAYOUT = -9         /* seq_lens and cu_seqlens both set for one axis */
+  SIGATTN_ERR_LAYOUT = -9,        /* seq_lens and cu_seqlens both set for one axis */
+  SIGATTN_ERR_WORKSPACE = -10     /* workspace smaller than sigattn_fwd_workspace_bytes, or misaligned */
 };
 
 /*
@@ -104,6 +105,22 @@ int sigattn_check(const sigattn_problem *p);
  * `stream` is a hipStream_t (NULL = default stream).
  */
 int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
+
+/*
+ * Split-KV forward for decode shapes (no counterpart in the reference, whose
+ * forward has one workgroup per 16..128 queries of a (batch, head) however
+ * few queries there are).  A non-causal problem with Tq <= 32 and Tk >= 256
+ * taking the MFMA kernels cuts each (batch, head)'s keys into chunks, one
+ * workgroup each, and sums the chunks' fp32 partials in a second kernel; the
+ * partials need sigattn_fwd_workspace_bytes(p) bytes of device memory
+ * (0 when the problem does not split).  sigattn_fwd_ws with workspace NULL (or
+ * sigattn_fwd) runs the same kernel with one chunk per (batch, head), so no
+ * workspace is touched.  The sum of fp32 partials is deterministic (fixed
+ * chunks, fixed order) and matches sigattn_fwd within fp32 summation order.
+ */
+size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p);
+int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
+                   void *stream);
 
 /*
  * Recompute backward: dq (q strides), dk and dv (k strides) from dout

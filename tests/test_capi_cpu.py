@@ -51,7 +51,7 @@ def test_abi_version_and_strerror():
     lib = _capi.load_library()
     assert lib.sigattn_abi_version() == _capi.ABI_VERSION
     assert lib.sigattn_strerror(0) == b"success"
-    for code in range(-9, 0):
+    for code in range(-10, 0):
         assert lib.sigattn_strerror(code) not in (b"", b"unknown sigattn status")
     assert lib.sigattn_strerror(-99) == b"unknown sigattn status"
 
@@ -125,6 +125,31 @@ def test_packed_layout_allows_different_lengths():
     assert lib.sigattn_check(ctypes.byref(p)) == 0
 
 
+def test_decode_workspace_size_and_errors():
+    """Split-KV forward (Tq <= 32, Tk >= 256, non-causal, MFMA dtypes): the
+    workspace size follows the plan, and a short or misaligned workspace is
+    rejected before any launch."""
+    lib = _capi.load_library()
+    D = 128
+    p = _problem(B=1, H=1, Tq=1, Tk=4096, D=D, seq_lens_q=1 << 20, seq_lens_k=1 << 20,
+                 q_stride_b=D, q_stride_t=D, q_stride_h=D, k_stride_b=4096 * D, k_stride_t=D, k_stride_h=D)
+    # 1 (batch, head) pair -> 16 chunks of 256 keys; fp32 partials [16, 1, 1, 1, D]
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 16 * D * 4
+    assert lib.sigattn_fwd_ws(ctypes.byref(p), 1 << 20, 1 << 20, 16 * D * 4 - 1, None) == -10
+    assert lib.sigattn_fwd_ws(ctypes.byref(p), 1 << 20, (1 << 20) + 4, 16 * D * 4, None) == -10
+    # No split: causal, Tq > 32, Tk < 256, fp32 -> no workspace.
+    for change in (dict(causal=1), dict(Tq=33), dict(Tk=255), dict(dtype=_capi.F32)):
+        q = _problem(B=1, H=1, Tq=1, Tk=4096, D=D, seq_lens_q=1 << 20, seq_lens_k=1 << 20)
+        for k, v in change.items():
+            setattr(q, k, v)
+        assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(q)) == 0, change
+    # Many (batch, head) pairs -> fewer chunks; invalid problems -> 0.
+    p.B, p.H = 16, 32
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 2 * 16 * 32 * D * 4
+    p.D = 48
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 0
+
+
 def test_empty_problems_return_before_any_launch():
     lib = _capi.load_library()
     for change in (dict(B=0), dict(H=0), dict(B=0, q=None, k=None, v=None, bias=None, scale=None)):
@@ -136,7 +161,7 @@ def test_empty_problems_return_before_any_launch():
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
-@pytest.mark.parametrize("src", ["fwd.hip", "bwd.hip", "generic.hip"])
+@pytest.mark.parametrize("src", ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip"])
 def test_device_code_has_no_packed_fp32_instructions(src):
     """Every HIP source is built with packed-fp32 selection disabled; check the
     gfx950 assembly of each kernel file."""

@@ -72,6 +72,36 @@ bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
   return true;
 }
 
+// Split-KV forward plan: nsplit = 0 when the main forward kernel takes the
+// problem.  Chunks are multiples of 128 keys (four waves of 32-key blocks),
+// at least 256 keys, and about SIGATTN_SPLIT_TARGET workgroups in all (no
+// split once the (batch, head) pairs alone reach that many).  Measured at
+// decode shapes, targets from 256 to 2048 workgroups run within noise of each
+// other; 512 keeps the partials small.
+struct SplitPlan {
+  int nsplit = 0, chunk = 0;
+};
+
+#ifndef SIGATTN_SPLIT_TARGET
+#define SIGATTN_SPLIT_TARGET 512
+#endif
+
+SplitPlan splitkv_plan(const sigattn_problem *p, bool mfma) {
+  SplitPlan sp;
+  if (!mfma || p->causal != 0 || p->Tq > 32 || p->Tk < 256 || p->B * p->H == 0) return sp;
+  const int64_t want = cdiv(SIGATTN_SPLIT_TARGET, p->B * p->H);
+  const int64_t most = cdiv(p->Tk, 256);
+  const int64_t n = want < most ? want : most;
+  const int64_t chunk = cdiv(cdiv(p->Tk, n), 128) * 128;
+  sp.nsplit = (int)cdiv(p->Tk, chunk);
+  sp.chunk = (int)chunk;
+  return sp;
+}
+
+int64_t splitkv_workspace_bytes(const sigattn_problem *p, const SplitPlan &sp) {
+  return sp.nsplit > 1 ? (int64_t)sp.nsplit * p->B * p->H * p->Tq * p->D * (int64_t)sizeof(float) : 0;
+}
+
 int launch_status() {
   return hipGetLastError() == hipSuccess ? SIGATTN_OK : SIGATTN_ERR_LAUNCH;
 }
@@ -96,6 +126,8 @@ const char *sigattn_strerror(int status) {
     case SIGATTN_ERR_LAUNCH: return "HIP kernel launch failed";
     case SIGATTN_ERR_LAYOUT:
       return "seq_lens and cu_seqlens cannot both be given for the same sequence axis";
+    case SIGATTN_ERR_WORKSPACE:
+      return "workspace smaller than sigattn_fwd_workspace_bytes() or not 16-byte aligned";
     default: return "unknown sigattn status";
   }
 }
@@ -130,7 +162,16 @@ int sigattn_check(const sigattn_problem *p) {
   return SIGATTN_OK;
 }
 
-int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
+size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p) {
+  if (sigattn_check(p) != SIGATTN_OK || p->B == 0 || p->H == 0 || p->Tq == 0) return 0;
+  // Pointers are not known yet: assume aligned rows (a misaligned call later
+  // takes the portable kernel and ignores the workspace).
+  const void *none[1] = {nullptr};
+  return (size_t)splitkv_workspace_bytes(p, splitkv_plan(p, use_mfma(p, none, 0)));
+}
+
+int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
+                   void *stream) {
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
   if (p->B == 0 || p->H == 0 || p->Tq == 0) return SIGATTN_OK;
@@ -139,12 +180,31 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
   k.out = out;
   const hipStream_t st = (hipStream_t)stream;
   const void *ptrs[4] = {p->q, p->k, p->v, out};
+  const bool mfma = use_mfma(p, ptrs, 4);
+  SplitPlan sp = splitkv_plan(p, mfma);
+  if (sp.nsplit > 1 && workspace != nullptr) {
+    if ((size_t)splitkv_workspace_bytes(p, sp) > workspace_bytes || !aligned16(workspace))
+      return SIGATTN_ERR_WORKSPACE;
+    k.ws = (float *)workspace;
+  } else if (sp.nsplit > 1) {
+    sp.nsplit = 1;  // no workspace: one chunk per (batch, head), written directly
+    sp.chunk = (int)(cdiv(p->Tk, 128) * 128);
+  }
   (void)hipGetLastError();
-  if (use_mfma(p, ptrs, 4))
+  if (sp.nsplit > 0) {
+    k.nsplit = sp.nsplit;
+    k.chunk = sp.chunk;
+    sigattn::launch_fwd_splitkv(k, p->dtype, (int)p->D, p->score_mod != nullptr, st);
+  } else if (mfma) {
     sigattn::launch_fwd_mfma(k, p->dtype, (int)p->D, p->causal != 0, p->score_mod != nullptr, st);
-  else
+  } else {
     sigattn::launch_fwd_generic(k, p->dtype, (int)p->D, p->causal != 0, st);
+  }
   return launch_status();
+}
+
+int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
+  return sigattn_fwd_ws(p, out, nullptr, 0, stream);
 }
 
 static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,

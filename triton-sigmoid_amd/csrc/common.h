@@ -82,6 +82,10 @@ struct KParams {
   int64_t sk_b, sk_t, sk_h;  // K / V / dK / dV
   int B, H, Tq, Tk;
   int nblk;  // number of row blocks along the stationary sequence axis
+  // Split-KV forward: keys cut into nsplit chunks of `chunk` keys; fp32
+  // partials [nsplit, B, H, Tq, D] in ws when nsplit > 1.
+  int nsplit, chunk;
+  float *ws;
 
   // Valid query / key rows of batch b.
   __device__ __forceinline__ int len_q(int b) const {

@@ -20,6 +20,11 @@ void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool sc
 void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
                           hipStream_t st);
 
+// Split-KV forward (decode shapes: Tq <= 32, non-causal) with the MFMA
+// kernels' requirements; p.nsplit / p.chunk set, p.ws holds
+// nsplit * B * H * Tq * D floats when nsplit > 1.
+void launch_fwd_splitkv(const KParams &p, int dtype, int D, bool scoremod, hipStream_t st);
+
 // Portable kernels: any dtype, D in {16, 32, 64, 128}, any alignment.
 void launch_fwd_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
 void launch_bwd_dq_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);

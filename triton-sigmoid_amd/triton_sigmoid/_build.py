@@ -20,7 +20,7 @@ INCLUDE = ROOT.parent / "include"
 LIB_PATH = PKG_DIR / "libsigattn.so"
 BUILD_DIR = ROOT / "_build"
 
-SOURCES = ["fwd.hip", "bwd.hip", "generic.hip", "capi.cpp"]
+SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "capi.cpp"]
 ARCH = "gfx950"
 
 

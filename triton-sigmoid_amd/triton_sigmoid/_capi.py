@@ -63,6 +63,8 @@ SIGNATURES = {
     "sigattn_strerror": ([_c_i32], ctypes.c_char_p),
     "sigattn_check": ([ctypes.POINTER(SigattnProblem)], _c_i32),
     "sigattn_fwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp], _c_i32),
+    "sigattn_fwd_workspace_bytes": ([ctypes.POINTER(SigattnProblem)], ctypes.c_size_t),
+    "sigattn_fwd_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, ctypes.c_size_t, _c_vp], _c_i32),
     "sigattn_bwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dq": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dkdv": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
@@ -177,6 +179,18 @@ def _prepare(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k):
     return Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k
 
 
+def _launch_fwd(lib, pr: SigattnProblem, out: torch.Tensor) -> None:
+    """sigattn_fwd_ws with the workspace the problem asks for (decode shapes
+    split their keys over several workgroups; others need none), allocated
+    from torch's caching allocator on the output's device."""
+    with torch.cuda.device(out.device):
+        stream = torch.cuda.current_stream(out.device).cuda_stream
+        nbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=out.device) if nbytes else None
+        rc = lib.sigattn_fwd_ws(ctypes.byref(pr), out.data_ptr(), _ptr(ws), nbytes, stream)
+        _raise(rc, "sigattn_fwd")
+
+
 def _raise(rc: int, what: str) -> None:
     if rc != 0:
         raise RuntimeError(f"{what} failed: {strerror(rc)} (status {rc})")
@@ -191,9 +205,7 @@ def forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) 
     if out.numel() == 0:
         return out
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
-    with torch.cuda.device(Q.device):
-        stream = torch.cuda.current_stream(Q.device).cuda_stream
-        _raise(lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream), "sigattn_fwd")
+    _launch_fwd(lib, pr, out)
     return out
 
 
@@ -243,9 +255,7 @@ def forward_packed(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
         return out
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
                   packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
-    with torch.cuda.device(Q.device):
-        stream = torch.cuda.current_stream(Q.device).cuda_stream
-        _raise(lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream), "sigattn_fwd")
+    _launch_fwd(lib, pr, out)
     return out
 
 
