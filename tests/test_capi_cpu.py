@@ -143,9 +143,12 @@ def test_decode_workspace_size_and_errors():
         for k, v in change.items():
             setattr(q, k, v)
         assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(q)) == 0, change
-    # Many (batch, head) pairs -> fewer chunks; invalid problems -> 0.
-    p.B, p.H = 16, 32
-    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 2 * 16 * 32 * D * 4
+    # More (batch, head) pairs -> fewer chunks (about 512 workgroups in all);
+    # from 512 pairs on nothing is split; invalid problems -> 0.
+    p.B, p.H = 8, 32
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 2 * 8 * 32 * D * 4
+    p.B = 16
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 0
     p.D = 48
     assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 0
 
