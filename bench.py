@@ -166,12 +166,20 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         pr = _capi._problem(q, k, v, bias, None, scale, seq_lens, seq_lens, cfg["causal"])
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
-    calls = {
-        "fwd": lambda: lib.sigattn_fwd(ctypes.byref(pr), o.data_ptr(), stream),
-        "bwd_dq": lambda: lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream),
-        "bwd_dkdv": lambda: lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
-                                                 dv.data_ptr(), stream),
-    }
+    calls = {"fwd": lambda: lib.sigattn_fwd(ctypes.byref(pr), o.data_ptr(), stream)}
+    # The backward the public API runs: two-pass (dK/dV storing dS, then dQ
+    # from dS) where _capi uses it, else the recompute kernels.
+    nbytes = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))) if D in _capi.TWO_PASS_HEAD_DIMS else 0
+    if 0 < nbytes <= _capi.bwd_workspace_limit():
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_dkdv_ws(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
+                                                            dv.data_ptr(), ws.data_ptr(), nbytes, stream)
+        calls["bwd_dq"] = lambda: lib.sigattn_bwd_dq_ws(ctypes.byref(pr), dq.data_ptr(), ws.data_ptr(), nbytes,
+                                                        stream)
+    else:
+        calls["bwd_dq"] = lambda: lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream)
+        calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
+                                                         dv.data_ptr(), stream)
     out = {}
     for name, fn in calls.items():
         for _ in range(3):
@@ -184,7 +192,10 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         e.record()
         e.synchronize()
         out[name] = s.elapsed_time(e) / iters
-    return out
+    if nbytes:
+        log(f"[bench] two-pass backward: dS workspace {nbytes / 1e9:.3f} GB; dQ-from-dS reads it at "
+            f"{nbytes / (out['bwd_dq'] * 1e-3) / 1e12:.2f} TB/s")
+    return {n: out[n] for n in ("fwd", "bwd_dq", "bwd_dkdv")}
 
 
 def cpu_baseline(cfg, budget_s: float = 20.0):

@@ -50,7 +50,7 @@ enum sigattn_status {
   SIGATTN_ERR_ABI_VERSION = -7,   /* problem.abi_version != SIGATTN_ABI_VERSION */
   SIGATTN_ERR_LAUNCH = -8,        /* hipGetLastError() reported a failure */
   SIGATTN_ERR_LAYOUT = -9,        /* seq_lens and cu_seqlens both set for one axis */
-  SIGATTN_ERR_WORKSPACE = -10     /* workspace smaller than sigattn_fwd_workspace_bytes, or misaligned */
+  SIGATTN_ERR_WORKSPACE = -10     /* workspace too small for the call, or misaligned */
 };
 
 /*
@@ -138,6 +138,39 @@ int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
 int sigattn_bwd_dq(const sigattn_problem *p, const void *dout, void *dq, void *stream);
 int sigattn_bwd_dkdv(const sigattn_problem *p, const void *dout, void *dk, void *dv,
                      void *stream);
+
+/*
+ * Two-pass backward (replaces the same two launches as sigattn_bwd,
+ * sigmoid_triton_dense.py:630-686 and sigmoid_triton_padded.py:706-770; the
+ * reference's dQ kernel recomputes S and dP, :162-307).  The dK/dV kernel
+ * also stores dS, rounded to the I/O dtype exactly as the dQ product consumes
+ * it, to a caller-owned workspace, and a second kernel computes
+ * dQ = dS·K·scale from it, so no matrix product is computed twice.  The
+ * workspace holds 2 bytes per (query, key) pair of every 32x32 block that has
+ * a visible pair (causal: the lower triangle), per batch and head:
+ * sigattn_bwd_workspace_bytes(p) for the whole problem, or 0 when the
+ * problem takes the portable kernels (fp32, D < 64, misaligned rows), which
+ * have no two-pass form.  sigattn_bwd_ws with a smaller workspace runs the
+ * heads in groups that fit, one group after another on `stream`; with room
+ * for less than one head, or workspace NULL, it runs sigattn_bwd.  Results
+ * equal sigattn_bwd's within fp32 summation order; the workspace must be
+ * 16-byte aligned and is only used until the call's kernels finish.
+ */
+size_t sigattn_bwd_workspace_bytes(const sigattn_problem *p);
+int sigattn_bwd_ws(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The two kernels of sigattn_bwd_ws, one launch each (used to time them one
+ * at a time).  Both need the whole problem's workspace
+ * (sigattn_bwd_workspace_bytes(p) bytes, else SIGATTN_ERR_WORKSPACE):
+ * sigattn_bwd_dkdv_ws stores dS there, and sigattn_bwd_dq_ws, called after
+ * it on the same stream with the same problem and workspace, reads it.
+ */
+int sigattn_bwd_dkdv_ws(const sigattn_problem *p, const void *dout, void *dk, void *dv,
+                        void *workspace, size_t workspace_bytes, void *stream);
+int sigattn_bwd_dq_ws(const sigattn_problem *p, void *dq, const void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -153,6 +153,46 @@ def test_decode_workspace_size_and_errors():
     assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(p)) == 0
 
 
+def test_two_pass_backward_workspace_size_and_errors():
+    """Two-pass backward: 2 KB per 32x32 (query, key) block per batch and
+    head, causal problems keeping the lower triangle only; 0 for problems the
+    portable kernels take.  Bad workspaces are rejected before any launch."""
+    lib = _capi.load_library()
+    D, T = 128, 100  # 4 blocks of 32 rows per axis
+    p = _problem(B=3, H=5, Tq=T, Tk=T, D=D, q_stride_b=T * 5 * D, q_stride_t=5 * D, q_stride_h=D,
+                 k_stride_b=T * 5 * D, k_stride_t=5 * D, k_stride_h=D)
+    assert lib.sigattn_bwd_workspace_bytes(ctypes.byref(p)) == 3 * 5 * 16 * 2048
+    p.causal = 1
+    assert lib.sigattn_bwd_workspace_bytes(ctypes.byref(p)) == 3 * 5 * 10 * 2048
+    p.causal = 0
+    p.Tk, p.seq_lens_k, p.seq_lens_q = 33, 1 << 20, 1 << 20  # cross: 4 x 2 blocks
+    assert lib.sigattn_bwd_workspace_bytes(ctypes.byref(p)) == 3 * 5 * 8 * 2048
+    for change in (dict(dtype=_capi.F32), dict(D=32), dict(q_stride_t=5 * D + 4), dict(Tq=0), dict(B=0),
+                   dict(D=48)):
+        q = _problem(B=3, H=5, Tq=T, Tk=T, D=D, q_stride_b=T * 5 * D, q_stride_t=5 * D, q_stride_h=D,
+                     k_stride_b=T * 5 * D, k_stride_t=5 * D, k_stride_h=D)
+        for k, v in change.items():
+            setattr(q, k, v)
+        assert lib.sigattn_bwd_workspace_bytes(ctypes.byref(q)) == 0, change
+    fake, nbytes = 1 << 20, 3 * 5 * 16 * 2048
+    p = _problem(B=3, H=5, Tq=T, Tk=T, D=D, q_stride_b=T * 5 * D, q_stride_t=5 * D, q_stride_h=D,
+                 k_stride_b=T * 5 * D, k_stride_t=5 * D, k_stride_h=D)
+    # misaligned workspace
+    assert lib.sigattn_bwd_ws(ctypes.byref(p), fake, fake, fake, fake, fake + 8, nbytes, None) == -10
+    # the halves need the whole problem's workspace, and a workspace at all
+    assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(p), fake, fake, fake, fake, nbytes - 1, None) == -10
+    assert lib.sigattn_bwd_dq_ws(ctypes.byref(p), fake, fake, nbytes - 2048, None) == -10
+    assert lib.sigattn_bwd_dq_ws(ctypes.byref(p), fake, None, nbytes, None) == -10
+    assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(p), fake, fake, fake, None, nbytes, None) == -10
+    # ... and a problem the two-pass kernels take (fp32 has none)
+    p.dtype = _capi.F32
+    assert lib.sigattn_bwd_dq_ws(ctypes.byref(p), fake, fake, nbytes, None) == -10
+    p.dtype = _capi.BF16
+    # null outputs are still reported first
+    assert lib.sigattn_bwd_ws(ctypes.byref(p), fake, None, fake, fake, fake, nbytes, None) == -1
+    assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(p), None, fake, fake, fake, nbytes, None) == -1
+
+
 def test_empty_problems_return_before_any_launch():
     lib = _capi.load_library()
     for change in (dict(B=0), dict(H=0), dict(B=0, q=None, k=None, v=None, bias=None, scale=None)):

@@ -1,0 +1,282 @@
+"""GPU tests of the two-pass backward (sigattn_bwd_ws): the dK/dV kernel stores
+dS to a workspace and dQ = dS·K·scale is read back from it.  The reference
+computes dQ in one kernel that recomputes S and dP
+(src/triton_sigmoid/sigmoid_triton_dense.py:162-307,
+sigmoid_triton_padded.py:179-339); the results must match the float64 oracle
+like the recompute backward's, dK and dV must equal the recompute backward's
+bit for bit (same kernel, which only adds the dS stores), and dQ must equal it
+within fp32 summation order.
+
+Every workspace here starts filled with 0xFF bytes (NaN in f16 and bf16), so
+a read of a dS tile the dK/dV pass did not store would put NaN into dQ."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ULP, assert_close_to_oracle, oracle_fwd_bwd, randn
+from triton_sigmoid import _capi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _problem(q, k, v, bias, scale, *, causal, seq_q=None, seq_k=None, score_mod=None, packed=None):
+    return _capi._problem(q, k, v, bias, score_mod, scale, seq_q, seq_k, causal, packed=packed)
+
+
+def _nan_workspace(nbytes):
+    return torch.full((max(nbytes, 16),), 0xFF, dtype=torch.uint8, device=DEV)
+
+
+def _bwd(pr, do, dq, dk, dv, ws=None, nbytes=0):
+    lib = _capi.load_library()
+    stream = torch.cuda.current_stream().cuda_stream
+    if ws is None:
+        rc = lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                             stream)
+    else:
+        rc = lib.sigattn_bwd_ws(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                ws.data_ptr(), nbytes, stream)
+    assert rc == 0, _capi.strerror(rc)
+    torch.cuda.synchronize()
+
+
+def _both(pr, q, k, do, ws_bytes=None):
+    """(recompute grads, two-pass grads); the two-pass call gets ws_bytes
+    bytes of workspace (default: the whole problem's)."""
+    lib = _capi.load_library()
+    full = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
+    assert full > 0
+    nbytes = full if ws_bytes is None else ws_bytes
+    ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    got = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd(pr, do, *ref)
+    _bwd(pr, do, *got, ws=_nan_workspace(nbytes), nbytes=nbytes)
+    return ref, got
+
+
+def _assert_twopass_matches(ref, got, dtype):
+    dq_r, dk_r, dv_r = ref
+    dq_g, dk_g, dv_g = got
+    assert torch.equal(dk_g, dk_r), "dK differs from the recompute backward"
+    assert torch.equal(dv_g, dv_r), "dV differs from the recompute backward"
+    assert torch.isfinite(dq_g).all(), "dQ has non-finite values (an unstored dS tile was read)"
+    # Same bf16/f16 dS values and keys; only the fp32 accumulation order may
+    # differ: a few units in the last place of the largest dQ.
+    err = (dq_g.float() - dq_r.float()).abs().max().item()
+    bound = 2 * ULP[dtype] * dq_r.float().abs().max().item() + 1e-6
+    assert err <= bound, f"dQ two-pass vs recompute: {err:.3e} > {bound:.3e}"
+
+
+def _dense_case(B, T, H, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [randn((B, T, H, D), dtype, DEV, g) for _ in range(4)]
+
+
+def _scalars(B, T, D, bias_value=None):
+    bias = torch.full((B,), -math.log(T) if bias_value is None else bias_value, dtype=torch.float32, device=DEV)
+    scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    return bias, scale
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [1, 31, 33, 130, 300, 577])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_twopass_matches_oracle_and_recompute(dtype, D, T, causal):
+    B, H = 2, 3
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=T * 13 + D + causal)
+    bias, scale = _scalars(B, T, D)
+    pr = _problem(q, k, v, bias, scale, causal=causal)
+    ref, got = _both(pr, q, k, do)
+    _assert_twopass_matches(ref, got, dtype)
+    _, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1 / math.sqrt(D)),
+                                      bias=bias.double().cpu().numpy(), causal=causal)
+    assert_close_to_oracle(got[0], dq, dtype, "dQ")
+    assert_close_to_oracle(got[1], dk, dtype, "dK")
+    assert_close_to_oracle(got[2], dv, dtype, "dV")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_score_mod_twopass(D, causal):
+    B, T, H = 2, 260, 2
+    dtype = torch.bfloat16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=41)
+    g = torch.Generator().manual_seed(42)
+    sm = torch.randn((B, T), generator=g).to(DEV)
+    bias, scale = _scalars(B, T, D, bias_value=-3.0)
+    pr = _problem(q, k, v, bias, scale, causal=causal, score_mod=sm)
+    ref, got = _both(pr, q, k, do)
+    _assert_twopass_matches(ref, got, dtype)
+    _, (dq, _, _) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1 / math.sqrt(D)), bias=np.full(B, -3.0),
+                                   score_mod=sm, causal=causal)
+    assert_close_to_oracle(got[0], dq, dtype, "dQ")
+
+
+def _padded_case(B, Tq, Tk, H, D, dtype, seed, lens_q, lens_k):
+    g = torch.Generator().manual_seed(seed)
+    q = randn((B, Tq, H, D), dtype, DEV, g)
+    k = randn((B, Tk, H, D), dtype, DEV, g)
+    v = randn((B, Tk, H, D), dtype, DEV, g)
+    do = randn((B, Tq, H, D), dtype, DEV, g)
+    sq = torch.tensor(lens_q, dtype=torch.int32)
+    sk = torch.tensor(lens_k, dtype=torch.int32)
+    for b in range(B):  # padding holds NaN: it must never be read
+        q[b, sq[b]:] = float("nan")
+        do[b, sq[b]:] = float("nan")
+        k[b, sk[b]:] = float("nan")
+        v[b, sk[b]:] = float("nan")
+    return q, k, v, do, sq, sk
+
+
+def _clean(t, lens):
+    t = t.detach().clone()
+    for b in range(t.shape[0]):
+        t[b, int(lens[b]):] = 0
+    return t
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Tq,Tk,lens_q,lens_k", [
+    (300, 300, [300, 1, 129, 0], [300, 1, 129, 5]),
+    (200, 333, [200, 64, 17, 33], [333, 300, 0, 31]),
+    (513, 96, [513, 480, 96, 2], [96, 64, 65, 1]),
+])
+def test_padded_twopass(D, causal, Tq, Tk, lens_q, lens_k):
+    if causal and Tq > Tk:
+        pytest.skip("top-left causal with more queries than keys is excluded, as in the reference tests")
+    dtype = torch.float16
+    B, H = 4, 2
+    q, k, v, do, sq, sk = _padded_case(B, Tq, Tk, H, D, dtype, seed=Tq + Tk + D, lens_q=lens_q, lens_k=lens_k)
+    bias = (-torch.log(sk.float().clamp(min=1))).to(DEV)
+    scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    # The problem holds raw pointers: the device tensors must outlive it.
+    sq_d, sk_d = sq.to(DEV), sk.to(DEV)
+    pr = _problem(q, k, v, bias, scale, causal=causal, seq_q=sq_d, seq_k=sk_d)
+    ref, got = _both(pr, q, k, do)
+    _, (dq, _, _) = oracle_fwd_bwd(_clean(q, sq), _clean(k, sk), _clean(v, sk), _clean(do, sq),
+                                   scale=np.float32(1 / math.sqrt(D)), bias=bias.double().cpu().numpy(),
+                                   seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    for b in range(B):  # per batch element, so a failure names the sequence lengths
+        for name, g_ in (("recompute", ref[0]), ("two-pass", got[0])):
+            assert_close_to_oracle(g_[b:b + 1], dq[b:b + 1], dtype,
+                                   f"{name} dQ of batch {b} (Lq={lens_q[b]}, Lk={lens_k[b]})")
+        assert torch.all(got[0][b, sq[b]:] == 0)
+    _assert_twopass_matches(ref, got, dtype)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_packed_twopass(causal):
+    D, H, dtype = 128, 2, torch.bfloat16
+    lens = [130, 1, 64, 257]
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    rows = int(cu[-1])
+    g = torch.Generator().manual_seed(77)
+    q, k, v, do = (randn((rows, H, D), dtype, DEV, g) for _ in range(4))
+    B = len(lens)
+    bias = (-torch.log(torch.tensor(lens, dtype=torch.float32))).to(DEV)
+    scale = torch.full((), 1.0 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    cu_d = cu.to(DEV)
+    pr = _problem(q, k, v, bias, scale, causal=causal, packed=(cu_d, cu_d, max(lens), max(lens)))
+    ref, got = _both(pr, q, k, do)
+    _assert_twopass_matches(ref, got, dtype)
+    for bi in range(B):  # each sequence against the dense oracle
+        s, e = int(cu[bi]), int(cu[bi + 1])
+        sl = lambda t: t[s:e].unsqueeze(0)  # noqa: E731
+        _, (dq, _, _) = oracle_fwd_bwd(sl(q), sl(k), sl(v), sl(do), scale=np.float32(1 / math.sqrt(D)),
+                                       bias=np.array([-math.log(lens[bi])]), causal=causal)
+        assert_close_to_oracle(got[0][s:e].unsqueeze(0), dq, dtype, f"dQ seq {bi}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_groups_equal_one_pass(causal):
+    """A workspace with room for fewer heads runs the heads in groups; the
+    results are the same bits as with the whole problem's workspace."""
+    B, T, H, D = 2, 333, 5, 128
+    dtype = torch.bfloat16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=5)
+    bias, scale = _scalars(B, T, D)
+    pr = _problem(q, k, v, bias, scale, causal=causal)
+    full = int(_capi.load_library().sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
+    per_head = full // H
+    _, whole = _both(pr, q, k, do)
+    for heads in (1, 2, 3):
+        _, part = _both(pr, q, k, do, ws_bytes=heads * per_head + per_head // 2)
+        for a, b_ in zip(whole, part):
+            assert torch.equal(a, b_), f"{heads} heads per pass"
+    # Room for less than one head: the recompute backward runs.
+    ref, small = _both(pr, q, k, do, ws_bytes=per_head - 2048)
+    for a, b_ in zip(ref, small):
+        assert torch.equal(a, b_)
+
+
+def test_halves_equal_whole():
+    """sigattn_bwd_dkdv_ws then sigattn_bwd_dq_ws give sigattn_bwd_ws's bits;
+    with less than the whole problem's workspace the halves refuse."""
+    B, T, H, D = 2, 500, 3, 128
+    dtype = torch.float16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=9)
+    bias, scale = _scalars(B, T, D)
+    pr = _problem(q, k, v, bias, scale, causal=True)
+    lib = _capi.load_library()
+    full = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
+    _, whole = _both(pr, q, k, do)
+    ws = _nan_workspace(full)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                                   full, stream) == 0
+    assert lib.sigattn_bwd_dq_ws(ctypes.byref(pr), dq.data_ptr(), ws.data_ptr(), full, stream) == 0
+    torch.cuda.synchronize()
+    for a, b_ in zip(whole, (dq, dk, dv)):
+        assert torch.equal(a, b_)
+    assert lib.sigattn_bwd_dq_ws(ctypes.byref(pr), dq.data_ptr(), ws.data_ptr(), full - 1, stream) == -10
+    assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(), dv.data_ptr(), None, 0,
+                                   stream) == -10
+
+
+def test_workspace_reuse_after_larger_problem():
+    """Tiles a smaller (padded) call does not store still hold the previous
+    call's dS; they must not be read."""
+    D, dtype = 128, torch.bfloat16
+    B, T, H = 2, 640, 2
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=3)
+    bias, scale = _scalars(B, T, D)
+    lib = _capi.load_library()
+    pr = _problem(q, k, v, bias, scale, causal=False)
+    full = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
+    ws = _nan_workspace(full)
+    g1 = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd(pr, do, *g1, ws=ws, nbytes=full)
+    sq = torch.tensor([100, 640], dtype=torch.int32, device=DEV)
+    sk = torch.tensor([37, 300], dtype=torch.int32, device=DEV)
+    pr2 = _problem(q, k, v, bias, scale, causal=False, seq_q=sq, seq_k=sk)
+    ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    got = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd(pr2, do, *ref)
+    _bwd(pr2, do, *got, ws=ws, nbytes=full)
+    _assert_twopass_matches(ref, got, dtype)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_public_api_uses_two_pass_at_d128(causal, monkeypatch):
+    """sigmoid_attention's backward at D = 128 takes the two-pass path (a
+    workspace is requested) and equals the recompute path with the workspace
+    limit set to 0."""
+    import triton_sigmoid as ts
+    B, T, H, D = 2, 384, 4, 128
+    dtype = torch.bfloat16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=21)
+    grads = []
+    for mb in ("2048", "0"):
+        monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", mb)
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        ts.sigmoid_attention(*leaves, is_causal=causal).backward(do)
+        grads.append([t.grad for t in leaves])
+    _assert_twopass_matches(grads[1], grads[0], dtype)

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 // (causal diagonal, seq_lens_q, pipeline fill) are applied to the packed
 // words of the few blocks that need them.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL, bool SCOREMOD>
+template <typename T, int D, bool CAUSAL, bool SCOREMOD, bool DSOUT>
 __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
   constexpr int BN = 128;                 // keys per workgroup (32 per wave)
   constexpr int BMQ = 64;                 // queries per LDS tile (two 32-query blocks)
@@ -358,6 +358,34 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     return g < 0 || qb0 + 32 > Lq || (CAUSAL && qb0 < kw + 31);
   };
 
+  // Two-pass backward: the masked dS words of block g (slot `slot`) become
+  // this wave's tile (query block mstart/32 + g, key block kw/32) of the dS
+  // workspace (DsLayout).  Tiles of queries past seq_lens_q, of keys past
+  // seq_lens_k, or (causal) wholly above the diagonal are not stored; the dQ
+  // pass reads none of them.
+  const int kbw = kw / 32;
+  uint16_t *ds_bh = nullptr;
+  if constexpr (DSOUT)
+    ds_bh = p.ds + ((int64_t)b * p.H + h) * DsLayout::per_bh(p.ds_nqb, p.ds_nkb, CAUSAL) *
+                       DsLayout::kTileElems;
+  // Every region issues exactly two store instructions, so the tile
+  // barrier can wait for its copies with a fixed vmcnt while the stores are
+  // still in flight: a skipped tile is a store through a buffer resource of
+  // zero bytes, which the hardware drops.
+  auto store_ds = [&](int slot, int g) SIGATTN_INLINE {
+    const int qb = mstart / 32 + g;
+    const bool ok = g >= 0 && 32 * qb < Lq && kw < Lk && (!CAUSAL || qb >= kbw);
+    // Buffer over query block qb's tiles up to and including this wave's.
+    const uint16_t *row = ds_bh + DsLayout::tile(ok ? qb : 0, 0, p.ds_nkb, CAUSAL) * DsLayout::kTileElems;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, ok ? (kbw + 1) * 2048 : 0, kBufferWord3);
+    const int off = kbw * 2048 + 16 * lane;
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[slot][0], dw[slot][1], dw[slot][2], dw[slot][3]}, rs,
+                                           off, 0, kStoreNT);
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[slot][4], dw[slot][5], dw[slot][6], dw[slot][7]}, rs,
+                                           off + 1024, 0, kStoreNT);
+  };
+
   // One region (U = r mod 8, so every slot and ring stage is static).
   auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
     constexpr int U = decltype(u_tag)::value;
@@ -376,12 +404,26 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
         // of the tile three back, whose last reads were two regions ago.
         const int t1 = (r + 1) / 2;
         if (t1 < ntiles) {
-          wait_dma();
+          if constexpr (DSOUT) {
+            // Tile t1's copies are older than the dS stores issued since
+            // (two per region; region 1 follows only region 0's), which may
+            // stay in flight.
+            if (r == 1) wait_vm<2>();
+            else wait_vm<4>();
+          } else {
+            wait_dma();
+          }
           asm volatile("" ::: "memory");
           __builtin_amdgcn_s_barrier();
           asm volatile("" ::: "memory");
           if (t1 + 1 < ntiles) issue((t1 + 1) % NST, t1 + 1);
         }
+      }
+      // dS of block r-2 (its words stay intact until the next region's
+      // VALU work), stored where the next vmcnt(0) is furthest away: at the
+      // start of even regions, after the tile barrier in odd ones.
+      if constexpr (DSOUT) {
+        if (((U % 2) == 0 && win == 0) || ((U % 2) == 1 && win * 4 == BAR)) store_ds(SL, r - 2);
       }
       // One wait for the window's four operands instead of one per MFMA.
       asm volatile("" ::"v"(opq[(win * 4) % LA]), "v"(opq[(win * 4 + 1) % LA]),
@@ -506,33 +548,282 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   }
 }
 
-#define SIGATTN_BWD_LAUNCHER(NAME, KERNEL, ROWBLK, ROWS, THREADS)                           \
-  template <typename T, int D>                                                              \
-  static void NAME##_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {           \
-    KParams p = kp;                                                                         \
-    p.nblk = ((ROWS) + (ROWBLK) - 1) / (ROWBLK);                                            \
-    const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(THREADS);                        \
-    if (causal) {                                                                           \
-      if (sm) KERNEL<T, D, true, true><<<grid, block, 0, st>>>(p);                          \
-      else KERNEL<T, D, true, false><<<grid, block, 0, st>>>(p);                            \
-    } else {                                                                                \
-      if (sm) KERNEL<T, D, false, true><<<grid, block, 0, st>>>(p);                         \
-      else KERNEL<T, D, false, false><<<grid, block, 0, st>>>(p);                           \
-    }                                                                                       \
-  }                                                                                         \
-  void NAME(const KParams &p, int dtype, int D, bool causal, bool sm, hipStream_t st) {     \
-    if (dtype == kBF16) {                                                                   \
-      if (D == 128) NAME##_t<__bf16, 128>(p, causal, sm, st);                               \
-      else NAME##_t<__bf16, 64>(p, causal, sm, st);                                         \
-    } else {                                                                                \
-      if (D == 128) NAME##_t<_Float16, 128>(p, causal, sm, st);                             \
-      else NAME##_t<_Float16, 64>(p, causal, sm, st);                                       \
-    }                                                                                       \
+// ---------------------------------------------------------------------------
+// dQ of the two-pass backward: dQ = dS · K · scale from the dS tiles the dK/dV
+// kernel stored (DsLayout), with no recomputation of S, P or dP.
+// Workgroup = 4 waves x 64 queries (two 32-query column blocks per wave);
+// keys stream in stages of KB 32-key blocks through an NST-stage LDS ring:
+// the K rows (shared by the waves) and each wave's own dS tiles (its two
+// query blocks x KB key blocks), all by direct global->LDS copies issued
+// NST-1 stages ahead, so about (NST-1) x (32 KB x KB dS + K) per CU is in
+// flight against HBM latency.
+//   dQᵀ[d, q] += Kᵀ[d, key] · dSᵀ[key, q]
+// A = Kᵀ via ds_read_b64_tr_b16 from the row-major K rows; B = dSᵀ via
+// ds_read_b64_tr_b16 from the dS tile, which the copy lays out key-major
+// (64 bytes per key: its four 16-byte pieces (g-pair c, query half h) at
+// slot 2c + h), so lane (query n, k-slot h) receives keys 16ks + 4h + {0..3}
+// and 16ks + 8 + 4h + {0..3} -- the same key order as the Kᵀ read.
+// Per 32 keys a wave reads 4 KB of dS and runs 16 MFMAs: the kernel is bound
+// by HBM bandwidth.
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL, int KB, int NST>
+__global__ __launch_bounds__(256, 1) void bwd_dq_ds_kernel(const KParams p) {
+  constexpr int BM = 256, BN = 32 * KB;
+  constexpr int NDB = D / 32;
+  constexpr int TE = DsLayout::kTileElems;
+  constexpr int KI = BN * D / 8 / 64 / 4;  // K-row copy instructions per wave and stage
+  constexpr int NI = KI + 4 * KB;          // copy instructions per wave and stage
+  constexpr int PF = NST - 1;              // stages in flight ahead of the one computed
+  static_assert(KI >= 1 && (NST - 2) * NI < 64, "stage shape");
+
+  __shared__ __attribute__((aligned(16))) uint16_t sK[NST][BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sS[NST][4 * 2 * KB * TE];
+
+  int b, h, qblk;
+  if (p.ragged() && p.B <= 64) {
+    const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
+    const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
+                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
+    b = it.b, h = it.h, qblk = it.blk;
+  } else {
+    const int BH = p.B * p.H;
+    const int bh = blockIdx.x % BH;
+    qblk = blockIdx.x / BH;
+    if (CAUSAL) qblk = p.nblk - 1 - qblk;  // heaviest query blocks first
+    b = bh / p.H, h = bh % p.H;
+  }
+  const int Lq = p.len_q(b);
+  const int Lk = p.len_k(b);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int q0 = qblk * BM;
+  const int qbw = q0 / 32 + 2 * w;  // the wave's two query blocks: qbw, qbw + 1
+  const int nqb_valid = (Lq + 31) / 32, nkb_valid = (Lk + 31) / 32;
+
+  const int64_t qoff = p.q_base(b, h);
+  const int64_t koff = p.k_base(b, h);
+  const uint16_t *Kb = (const uint16_t *)p.k + koff;
+  uint16_t *dQb = (uint16_t *)p.dq + qoff;
+  const uint16_t *ds_bh = p.ds + ((int64_t)b * p.H + h) * DsLayout::per_bh(p.ds_nqb, p.ds_nkb, CAUSAL) * TE;
+
+  int nend = Lk;
+  if (CAUSAL) nend = min(nend, min(q0 + BM, Lq));
+  if (q0 >= Lq) nend = 0;
+  const int ntiles = (nend + BN - 1) / BN;
+
+  // Tile (query block qb, key block kb) was stored by the dK/dV pass.
+  auto tile_ok = [&](int qb, int kb) SIGATTN_INLINE {
+    return qb < nqb_valid && kb < nkb_valid && (!CAUSAL || kb <= qb);
+  };
+
+  TileOffsets<D> to;
+  to.init(lane);
+  DmaPlan<BN, D, 4> dma;
+  dma.init(w, lane);
+  const int kv_stride_bytes = (int)(p.sk_t * 2);
+
+  // Copy of a dS tile: instruction i fills keys 16i .. 16i+15 (1 KB); lane
+  // j lands at key 16i + j/4, slot j%4 = (g-pair c, half h) and fetches
+  // piece c of the stored lane 32h + key (at 1024 c + 16 (32h + key)).
+  uint32_t soff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int key = 16 * i + lane / 4, s = lane % 4;
+    soff[i] = (uint32_t)((s >> 1) * 1024 + 16 * ((s & 1) * 32 + key));
+  }
+  // dSᵀ operand read: lane (group g16, s = 4e + m) reads key 16ks + 4h + e
+  // (+8 for the second half), queries 4M .. 4M+3 with M = 4(g16 & 1) + m.
+  int boff;
+  {
+    const int g16 = lane >> 4, s = lane & 15, e = s >> 2, m = s & 3, hh = g16 >> 1;
+    boff = 32 * (4 * hh + e) + 8 * (2 * (g16 & 1) + (m & 1)) + 4 * (m >> 1);
+  }
+  auto ld_ds = [&](const uint16_t *tile, int ks) SIGATTN_INLINE {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const uint16_t *base = tile + 512 * ks + boff;
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)base);
+    const s16x4 c = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4 *)(base + 256));
+    const u32x2 lo = __builtin_bit_cast(u32x2, a);
+    const u32x2 hv = __builtin_bit_cast(u32x2, c);
+    return (u32x4){lo.x, lo.y, hv.x, hv.y};
+  };
+  // LDS slot of the wave's tile (column block cb, key block kl of the stage).
+  auto ds_slot = [&](int st, int cb, int kl) SIGATTN_INLINE {
+    return &sS[st][((4 * w + 2 * cb) * KB + 2 * kl) * TE / 2];
+  };
+
+  auto issue = [&](int st, int u) SIGATTN_INLINE {
+    dma.issue(sK[st], Kb, kv_stride_bytes, u * BN, Lk);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int kl = 0; kl < KB; ++kl) {
+        const int qb = qbw + cb, kb = KB * u + kl;
+        // Tiles the dK/dV pass did not store are replaced by tile 0 of this
+        // (batch, head) (in bounds; their products are skipped).
+        const int64_t ti = tile_ok(qb, kb) ? DsLayout::tile(qb, kb, p.ds_nkb, CAUSAL) : 0;
+        const uint16_t *src = ds_bh + ti * TE;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          uint16_t *dst = ds_slot(st, cb, kl) + 512 * i;
+          const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+          asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                       :
+                       : "v"(soff[i]), "s"(src), "{m0}"(m0)
+                       : "memory");
+        }
+      }
+    }
+  };
+
+  f32x16 acc[2][NDB];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int d = 0; d < NDB; ++d) acc[c][d] = zero16();
+
+  // Every MFMA runs on every stage: a tile the dK/dV pass did not store
+  // enters as a zero operand (the K rows are finite, so it adds exactly 0).
+  // Branching around the products instead makes the compiler copy all the
+  // accumulators at every join.
+  auto compute = [&](int st, int u) SIGATTN_INLINE {
+#pragma unroll
+    for (int kl = 0; kl < KB; ++kl) {
+      const int kb = KB * u + kl;
+      const bool ok0 = tile_ok(qbw, kb), ok1 = tile_ok(qbw + 1, kb);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ks = 2 * kl + j;
+        u32x4 b0 = ld_ds(ds_slot(st, 0, kl), j);
+        u32x4 b1 = ld_ds(ds_slot(st, 1, kl), j);
+        b0 = ok0 ? b0 : zero4();
+        b1 = ok1 ? b1 : zero4();
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const u32x4 a = ld_tr<D>(sK[st], to, ks, db);
+          acc[0][db] = Elem<T>::mfma(a, b0, acc[0][db]);
+          acc[1][db] = Elem<T>::mfma(a, b1, acc[1][db]);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (u < ntiles) issue(u, u);
+  for (int u = 0; u < ntiles; ++u) {
+    // Wait for this wave's copies of stage u (the later stages' copies may
+    // stay in flight), then for every wave's.
+    wait_vm_steps<NI, PF - 1>(min(ntiles - 1 - u, PF - 1));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // The stage the copy fills last held stage u-1, which every wave has
+    // finished reading (they all passed the barrier above after computing it).
+    if (u + PF < ntiles) issue((u + PF) % NST, u + PF);
+    compute(u % NST, u);
   }
 
-SIGATTN_BWD_LAUNCHER(launch_bwd_dq_mfma, bwd_dq_kernel, 128, p.Tq, 256)
-SIGATTN_BWD_LAUNCHER(launch_bwd_dkdv_mfma, bwd_dkdv_kernel, 128, p.Tk, 256)
+  const float scale = *p.scale;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int my_q = q0 + 64 * w + 32 * c + l32;
+    if (my_q < p.q_rows_out(Lq)) {
+      uint16_t *row = dQb + (int64_t)my_q * p.sq_t;
+      const bool valid = my_q < Lq;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = db * 32 + 8 * g + 4 * hi;
+          u32x2 o;
+          o.x = Elem<T>::pack(acc[c][db][4 * g] * scale, acc[c][db][4 * g + 1] * scale);
+          o.y = Elem<T>::pack(acc[c][db][4 * g + 2] * scale, acc[c][db][4 * g + 3] * scale);
+          if (!valid) o = (u32x2){0u, 0u};
+          *(u32x2 *)(row + d0) = o;
+        }
+      }
+    }
+  }
+}
 
-#undef SIGATTN_BWD_LAUNCHER
+template <int ROWBLK, typename Launch>
+static void launch_rows(const KParams &kp, int rows, Launch &&launch) {
+  KParams p = kp;
+  p.nblk = (rows + ROWBLK - 1) / ROWBLK;
+  launch(p, dim3((unsigned)(p.nblk * p.B * p.H)));
+}
+
+template <typename T, int D>
+static void bwd_dq_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
+  launch_rows<128>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+    if (causal) {
+      if (sm) bwd_dq_kernel<T, D, true, true><<<grid, 256, 0, st>>>(p);
+      else bwd_dq_kernel<T, D, true, false><<<grid, 256, 0, st>>>(p);
+    } else {
+      if (sm) bwd_dq_kernel<T, D, false, true><<<grid, 256, 0, st>>>(p);
+      else bwd_dq_kernel<T, D, false, false><<<grid, 256, 0, st>>>(p);
+    }
+  });
+}
+
+template <typename T, int D, bool DSOUT>
+static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
+  launch_rows<128>(kp, kp.Tk, [&](const KParams &p, dim3 grid) {
+    if (causal) {
+      if (sm) bwd_dkdv_kernel<T, D, true, true, DSOUT><<<grid, 256, 0, st>>>(p);
+      else bwd_dkdv_kernel<T, D, true, false, DSOUT><<<grid, 256, 0, st>>>(p);
+    } else {
+      if (sm) bwd_dkdv_kernel<T, D, false, true, DSOUT><<<grid, 256, 0, st>>>(p);
+      else bwd_dkdv_kernel<T, D, false, false, DSOUT><<<grid, 256, 0, st>>>(p);
+    }
+  });
+}
+
+template <typename T, int D>
+static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
+  launch_rows<256>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+    // One 32-key block per stage in a 6-stage ring: 5 stages (about 120 KB per
+    // CU) in flight.
+    if (causal) bwd_dq_ds_kernel<T, D, true, 1, 6><<<grid, 256, 0, st>>>(p);
+    else bwd_dq_ds_kernel<T, D, false, 1, 6><<<grid, 256, 0, st>>>(p);
+  });
+}
+
+// dtype in {kF16, kBF16}, D in {64, 128}.
+template <class F>
+static void by_type(int dtype, int D, F &&f) {
+  if (dtype == kBF16) {
+    if (D == 128) f((__bf16 *)nullptr, std::integral_constant<int, 128>{});
+    else f((__bf16 *)nullptr, std::integral_constant<int, 64>{});
+  } else {
+    if (D == 128) f((_Float16 *)nullptr, std::integral_constant<int, 128>{});
+    else f((_Float16 *)nullptr, std::integral_constant<int, 64>{});
+  }
+}
+
+void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool sm, hipStream_t st) {
+  by_type(dtype, D, [&](auto *t, auto d) {
+    bwd_dq_t<std::remove_pointer_t<decltype(t)>, decltype(d)::value>(p, causal, sm, st);
+  });
+}
+
+void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool sm, bool dsout,
+                          hipStream_t st) {
+  by_type(dtype, D, [&](auto *t, auto d) {
+    using T = std::remove_pointer_t<decltype(t)>;
+    if (dsout) bwd_dkdv_t<T, decltype(d)::value, true>(p, causal, sm, st);
+    else bwd_dkdv_t<T, decltype(d)::value, false>(p, causal, sm, st);
+  });
+}
+
+void launch_bwd_dq_ds_mfma(const KParams &p, int dtype, int D, bool causal, hipStream_t st) {
+  by_type(dtype, D, [&](auto *t, auto d) {
+    bwd_dq_ds_t<std::remove_pointer_t<decltype(t)>, decltype(d)::value>(p, causal, st);
+  });
+}
 
 }  // namespace sigattn

@@ -102,6 +102,33 @@ int64_t splitkv_workspace_bytes(const sigattn_problem *p, const SplitPlan &sp) {
   return sp.nsplit > 1 ? (int64_t)sp.nsplit * p->B * p->H * p->Tq * p->D * (int64_t)sizeof(float) : 0;
 }
 
+// Two-pass backward: bytes of dS tiles (DsLayout) per head, over all batches.
+int64_t ds_bytes_per_head(const sigattn_problem *p) {
+  const int64_t nqb = cdiv(p->Tq, 32), nkb = cdiv(p->Tk, 32);
+  const int64_t tiles = p->causal != 0 ? nqb * (nqb + 1) / 2 : nqb * nkb;
+  return p->B * tiles * 2048;
+}
+
+// The sub-problem of heads [h0, h0 + nh): every tensor is [.., H, D] with
+// its own head stride, so the heads are a pointer offset away; bias,
+// score_mod and the sequence lengths are per batch and stay as they are.
+KParams head_slice(const KParams &k, int64_t h0, int64_t nh, int64_t esize) {
+  KParams s = k;
+  const int64_t qo = h0 * k.sq_h * esize, ko = h0 * k.sk_h * esize;
+  auto adv = [](const void *ptr, int64_t off) -> const char * {
+    return ptr == nullptr ? nullptr : (const char *)ptr + off;
+  };
+  s.q = adv(k.q, qo);
+  s.dout = adv(k.dout, qo);
+  s.dq = (void *)adv(k.dq, qo);
+  s.k = adv(k.k, ko);
+  s.v = adv(k.v, ko);
+  s.dk = (void *)adv(k.dk, ko);
+  s.dv = (void *)adv(k.dv, ko);
+  s.H = (int)nh;
+  return s;
+}
+
 int launch_status() {
   return hipGetLastError() == hipSuccess ? SIGATTN_OK : SIGATTN_ERR_LAUNCH;
 }
@@ -127,7 +154,7 @@ const char *sigattn_strerror(int status) {
     case SIGATTN_ERR_LAYOUT:
       return "seq_lens and cu_seqlens cannot both be given for the same sequence axis";
     case SIGATTN_ERR_WORKSPACE:
-      return "workspace smaller than sigattn_fwd_workspace_bytes() or not 16-byte aligned";
+      return "workspace too small for the call or not 16-byte aligned";
     default: return "unknown sigattn status";
   }
 }
@@ -207,53 +234,116 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
   return sigattn_fwd_ws(p, out, nullptr, 0, stream);
 }
 
+// Which kernels a backward call runs.
+enum BwdParts { kBwdAll, kBwdDq, kBwdDkdv };
+
 static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
-                    void *stream, bool do_dq, bool do_dkdv) {
+                    void *workspace, size_t workspace_bytes, void *stream, BwdParts parts) {
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
+  if (workspace != nullptr && !aligned16(workspace)) return SIGATTN_ERR_WORKSPACE;
   if (p->B == 0 || p->H == 0) return SIGATTN_OK;
-  const bool need_dq = do_dq && p->Tq > 0;
-  const bool need_dkdv = do_dkdv && p->Tk > 0;
+  const bool need_dq = parts != kBwdDkdv && p->Tq > 0;
+  const bool need_dkdv = parts != kBwdDq && p->Tk > 0;
+  const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
+  const bool mfma = use_mfma(p, ptrs, 7);
+
+  // Two-pass backward when a workspace holds the dS of at least one head.
+  // The halves (kBwdDq, kBwdDkdv) need the whole problem's dS at once: the
+  // dQ half reads what a dK/dV half with the same workspace stored.
+  int64_t heads_per_pass = 0;
+  if (workspace != nullptr && mfma && p->Tq > 0 && p->Tk > 0) {
+    heads_per_pass = (int64_t)workspace_bytes / ds_bytes_per_head(p);
+    if (heads_per_pass > p->H) heads_per_pass = p->H;
+  }
+  if (parts != kBwdAll && workspace != nullptr) {
+    if (!mfma) return SIGATTN_ERR_WORKSPACE;  // no two-pass kernels for this problem
+    if (p->Tq > 0 && p->Tk > 0 && heads_per_pass < p->H) return SIGATTN_ERR_WORKSPACE;
+  }
+  const bool twopass = heads_per_pass > 0;
+
   if (need_dq && dq == nullptr) return SIGATTN_ERR_NULL_ARG;
   if (need_dkdv && (dk == nullptr || dv == nullptr)) return SIGATTN_ERR_NULL_ARG;
-  if ((need_dq || need_dkdv) && p->Tq > 0 && dout == nullptr) return SIGATTN_ERR_NULL_ARG;
+  // dO feeds every kernel except the dQ-from-dS one.
+  const bool need_dout = need_dkdv || (need_dq && !(twopass && parts == kBwdDq));
+  if (need_dout && p->Tq > 0 && dout == nullptr) return SIGATTN_ERR_NULL_ARG;
+
   KParams k = make_params(p);
   k.dout = dout;
   k.dq = dq;
   k.dk = dk;
   k.dv = dv;
   const hipStream_t st = (hipStream_t)stream;
-  const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
-  const bool mfma = use_mfma(p, ptrs, 7);
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
+  const int dt = p->dtype, D = (int)p->D;
   (void)hipGetLastError();
-  // Both kernels go on the caller's stream, one after the other: each fills
-  // the GPU on its own and they cannot share a CU (their LDS footprints add
-  // up to more than one CU holds), so running them concurrently on two
-  // streams only made both slower (measured).
+  if (twopass) {
+    k.ds = (uint16_t *)workspace;
+    k.ds_nqb = (int)cdiv(p->Tq, 32);
+    k.ds_nkb = (int)cdiv(p->Tk, 32);
+    // Per head group: dK/dV (storing dS), then dQ from dS, on one stream, so
+    // the next group's dK/dV overwrites the workspace only after this
+    // group's dQ has read it.
+    for (int64_t h0 = 0; h0 < p->H; h0 += heads_per_pass) {
+      const int64_t nh = p->H - h0 < heads_per_pass ? p->H - h0 : heads_per_pass;
+      const KParams s = head_slice(k, h0, nh, 2);
+      if (parts != kBwdDq) sigattn::launch_bwd_dkdv_mfma(s, dt, D, causal, sm, true, st);
+      if (parts != kBwdDkdv) sigattn::launch_bwd_dq_ds_mfma(s, dt, D, causal, st);
+    }
+    return launch_status();
+  }
+  // Recompute backward.  Both kernels go on the caller's stream, one after
+  // the other: each fills the GPU on its own and they cannot share a CU
+  // (their LDS footprints add up to more than one CU holds), so running them
+  // concurrently on two streams only made both slower (measured).
   if (need_dq) {
-    if (mfma) sigattn::launch_bwd_dq_mfma(k, p->dtype, (int)p->D, causal, sm, st);
-    else sigattn::launch_bwd_dq_generic(k, p->dtype, (int)p->D, causal, st);
+    if (mfma) sigattn::launch_bwd_dq_mfma(k, dt, D, causal, sm, st);
+    else sigattn::launch_bwd_dq_generic(k, dt, D, causal, st);
   }
   if (need_dkdv) {
-    if (mfma) sigattn::launch_bwd_dkdv_mfma(k, p->dtype, (int)p->D, causal, sm, st);
-    else sigattn::launch_bwd_dkdv_generic(k, p->dtype, (int)p->D, causal, st);
+    if (mfma) sigattn::launch_bwd_dkdv_mfma(k, dt, D, causal, sm, false, st);
+    else sigattn::launch_bwd_dkdv_generic(k, dt, D, causal, st);
   }
   return launch_status();
 }
 
+size_t sigattn_bwd_workspace_bytes(const sigattn_problem *p) {
+  if (sigattn_check(p) != SIGATTN_OK || p->B == 0 || p->H == 0 || p->Tq == 0 || p->Tk == 0) return 0;
+  const void *none[1] = {nullptr};
+  if (!use_mfma(p, none, 0)) return 0;
+  return (size_t)(ds_bytes_per_head(p) * p->H);
+}
+
+int sigattn_bwd_ws(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  return bwd_impl(p, dout, dq, dk, dv, workspace, workspace_bytes, stream, kBwdAll);
+}
+
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
                 void *stream) {
-  return bwd_impl(p, dout, dq, dk, dv, stream, true, true);
+  return bwd_impl(p, dout, dq, dk, dv, nullptr, 0, stream, kBwdAll);
 }
 
 int sigattn_bwd_dq(const sigattn_problem *p, const void *dout, void *dq, void *stream) {
-  return bwd_impl(p, dout, dq, nullptr, nullptr, stream, true, false);
+  return bwd_impl(p, dout, dq, nullptr, nullptr, nullptr, 0, stream, kBwdDq);
 }
 
 int sigattn_bwd_dkdv(const sigattn_problem *p, const void *dout, void *dk, void *dv,
                      void *stream) {
-  return bwd_impl(p, dout, nullptr, dk, dv, stream, false, true);
+  return bwd_impl(p, dout, nullptr, dk, dv, nullptr, 0, stream, kBwdDkdv);
+}
+
+int sigattn_bwd_dkdv_ws(const sigattn_problem *p, const void *dout, void *dk, void *dv,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+  if (workspace == nullptr) return SIGATTN_ERR_WORKSPACE;
+  return bwd_impl(p, dout, nullptr, dk, dv, workspace, workspace_bytes, stream, kBwdDkdv);
+}
+
+int sigattn_bwd_dq_ws(const sigattn_problem *p, void *dq, const void *workspace,
+                      size_t workspace_bytes, void *stream) {
+  if (workspace == nullptr) return SIGATTN_ERR_WORKSPACE;
+  return bwd_impl(p, nullptr, dq, nullptr, nullptr, (void *)workspace, workspace_bytes, stream,
+                  kBwdDq);
 }
 
 }  // extern "C"

@@ -86,6 +86,10 @@ struct KParams {
   // partials [nsplit, B, H, Tq, D] in ws when nsplit > 1.
   int nsplit, chunk;
   float *ws;
+  // Two-pass backward: dS in the I/O dtype as 32x32 tiles (see DsLayout),
+  // written by the dK/dV kernel and read by the dQ-from-dS kernel.
+  uint16_t *ds;
+  int ds_nqb, ds_nkb;  // 32-row query / key blocks per (batch, head): ceil(Tq/32), ceil(Tk/32)
 
   // Valid query / key rows of batch b.
   __device__ __forceinline__ int len_q(int b) const {
@@ -204,6 +208,28 @@ struct WorkOrder {
       base += cnt;
     }
     return padding(id - base, B, H, nv, nlev);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// dS workspace of the two-pass backward.  dS of (batch, head) is cut into
+// 32-query x 32-key tiles of 2 KB.  Causal problems keep only the tiles that
+// hold a visible pair (key block <= query block), stored as a lower triangle
+// row by row; the others keep the full [query block][key block] rectangle.
+// Inside a tile, lane l of the dK/dV kernel's accumulator layout (key l % 32,
+// query half h = l / 32) holds the 16-bit dS of queries {8g + 4h + i : g =
+// 0..3, i = 0..3}; piece c (g = 2c, 2c + 1, 16 bytes in (g, i) order) is
+// stored at byte 1024 c + 16 l, so each of the two store instructions writes
+// 1 KB of whole cache lines, and each group of four consecutive queries of one
+// key is one aligned 8-byte word.
+struct DsLayout {
+  static constexpr int kTileElems = 1024;
+  static __device__ __forceinline__ int64_t per_bh(int nqb, int nkb, bool causal) {
+    return causal ? (int64_t)nqb * (nqb + 1) / 2 : (int64_t)nqb * nkb;
+  }
+  // Tile index of (query block qb, key block kb) relative to the (b, h) base.
+  static __device__ __forceinline__ int64_t tile(int qb, int kb, int nkb, bool causal) {
+    return causal ? (int64_t)qb * (qb + 1) / 2 + kb : (int64_t)qb * nkb + kb;
   }
 };
 
@@ -406,6 +432,35 @@ template <int ROWS, int D, int NWAVES> struct DmaPlan {
 };
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Waits until at most N vector-memory operations of this wave are in flight
+// (they complete in issue order, so everything older than the N most recent
+// has completed).
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+}
+
+// Waits until at most n * STEP operations are in flight (0 <= n <= N, n known
+// only at run time).
+template <int STEP, int N> __device__ __forceinline__ void wait_vm_steps(int n) {
+  if constexpr (N == 0) {
+    wait_vm<0>();
+  } else {
+    if (n >= N) wait_vm<N * STEP>();
+    else wait_vm_steps<STEP, N - 1>(n);
+  }
+}
+
+// Word 3 of a gfx9 buffer resource for raw (untyped, stride 0) access:
+// accesses at or past num_records bytes are dropped.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer builtins: non-temporal (streaming) store,
+// for data the writing kernel never reads back (measured: the dS stream of
+// the two-pass backward costs the dK/dV kernel 0.10 ms at the headline shape
+// with it, 0.16 ms without).
+constexpr int kStoreNT = 2;
 
 // Per-lane element offsets into swizzled [*, D] tiles, computed once per
 // kernel.  A row offset that is a multiple of 16 rows leaves swz() unchanged,

@@ -18,7 +18,10 @@ void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool score
 void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
                         hipStream_t st);
 void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
-                          hipStream_t st);
+                          bool dsout, hipStream_t st);
+// dQ = dS·K·scale from the dS tiles a launch_bwd_dkdv_mfma(dsout = true) on
+// the same problem stored in p.ds (two-pass backward).
+void launch_bwd_dq_ds_mfma(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
 
 // Split-KV forward (decode shapes: Tq <= 32, non-causal) with the MFMA
 // kernels' requirements; p.nsplit / p.chunk set, p.ws holds

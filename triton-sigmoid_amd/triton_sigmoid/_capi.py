@@ -9,6 +9,7 @@ the built library or a gfx950 device the call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 from typing import Optional
@@ -68,6 +69,12 @@ SIGNATURES = {
     "sigattn_bwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dq": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dkdv": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
+    "sigattn_bwd_workspace_bytes": ([ctypes.POINTER(SigattnProblem)], ctypes.c_size_t),
+    "sigattn_bwd_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_size_t,
+                        _c_vp], _c_i32),
+    "sigattn_bwd_dkdv_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_size_t,
+                             _c_vp], _c_i32),
+    "sigattn_bwd_dq_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, ctypes.c_size_t, _c_vp], _c_i32),
 }
 
 _lib = None
@@ -191,6 +198,38 @@ def _launch_fwd(lib, pr: SigattnProblem, out: torch.Tensor) -> None:
         _raise(rc, "sigattn_fwd")
 
 
+# Two-pass backward (dS stored by the dK/dV kernel, dQ = dS·K read back):
+# head dims it is used for, and the most workspace it may take (larger
+# problems run their heads in groups that fit).  At D = 128 it replaces the dQ
+# kernel's 4·D-FLOP recomputation of S and dP per pair with 2 bytes of dS
+# written and read back.
+TWO_PASS_HEAD_DIMS = (128,)
+_WS_ENV = "SIGATTN_BWD_WORKSPACE_MB"
+_WS_DEFAULT_MB = 2048
+
+
+def bwd_workspace_limit() -> int:
+    """Largest two-pass backward workspace in bytes (0 disables the path);
+    environment variable SIGATTN_BWD_WORKSPACE_MB, default 2048."""
+    raw = os.environ.get(_WS_ENV)
+    mb = _WS_DEFAULT_MB if raw is None or raw.strip() == "" else int(raw)
+    return max(mb, 0) << 20
+
+
+def _launch_bwd(lib, pr: SigattnProblem, dO, dQ, dK, dV) -> None:
+    """sigattn_bwd_ws with a workspace from torch's caching allocator when
+    the two-pass backward applies (see TWO_PASS_HEAD_DIMS), else sigattn_bwd."""
+    with torch.cuda.device(dQ.device):
+        stream = torch.cuda.current_stream(dQ.device).cuda_stream
+        nbytes = 0
+        if pr.D in TWO_PASS_HEAD_DIMS:
+            nbytes = min(int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))), bwd_workspace_limit())
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dQ.device) if nbytes else None
+        rc = lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
+                                stream)
+        _raise(rc, "sigattn_bwd_ws")
+
+
 def _raise(rc: int, what: str) -> None:
     if rc != 0:
         raise RuntimeError(f"{what} failed: {strerror(rc)} (status {rc})")
@@ -210,7 +249,9 @@ def forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) 
 
 
 def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):
-    """(dQ, dK, dV) via sigattn_bwd (dQ kernel, then dK/dV kernel)."""
+    """(dQ, dK, dV) via sigattn_bwd_ws: the two-pass backward (dK/dV kernel
+    storing dS, then dQ from dS) where it applies, else the recompute backward
+    (dQ kernel, then dK/dV kernel)."""
     lib = load_library()
     Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k = _prepare(
         Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
@@ -221,10 +262,7 @@ def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, cau
     if dQ.numel() == 0 and dK.numel() == 0:
         return dQ, dK, dV
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
-    with torch.cuda.device(Q.device):
-        stream = torch.cuda.current_stream(Q.device).cuda_stream
-        rc = lib.sigattn_bwd(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), stream)
-        _raise(rc, "sigattn_bwd")
+    _launch_bwd(lib, pr, dO, dQ, dK, dV)
     return dQ, dK, dV
 
 
@@ -261,7 +299,7 @@ def forward_packed(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
 
 def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, bias, score_mod,
                     sm_scale, causal):
-    """(dQ, dK, dV) for packed [rows, H, D] tensors via sigattn_bwd."""
+    """(dQ, dK, dV) for packed [rows, H, D] tensors via sigattn_bwd_ws."""
     lib = load_library()
     Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
     cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
@@ -273,8 +311,5 @@ def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_s
         return dQ, dK, dV
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
                   packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
-    with torch.cuda.device(Q.device):
-        stream = torch.cuda.current_stream(Q.device).cuda_stream
-        rc = lib.sigattn_bwd(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), stream)
-        _raise(rc, "sigattn_bwd")
+    _launch_bwd(lib, pr, dO, dQ, dK, dV)
     return dQ, dK, dV
