@@ -166,7 +166,12 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         pr = _capi._problem(q, k, v, bias, None, scale, seq_lens, seq_lens, cfg["causal"])
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
-    calls = {"fwd": lambda: lib.sigattn_fwd(ctypes.byref(pr), o.data_ptr(), stream)}
+    # The forward the public API runs: with the workspace the library asks
+    # for (split-KV decode, or the split forward of ragged problems).
+    fbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
+    fws = torch.empty(max(fbytes, 16), dtype=torch.uint8, device=q.device)
+    calls = {"fwd": lambda: lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), fws.data_ptr() if fbytes else None,
+                                               fbytes, stream)}
     # The backward the public API runs: two-pass (dK/dV storing dS, then dQ
     # from dS) where _capi uses it, else the recompute kernels.
     nbytes = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))) if D in _capi.TWO_PASS_HEAD_DIMS else 0
@@ -493,9 +498,13 @@ def main():
                           seq_lens=sl, packed=True)
         packed_tf = 14 * D * P / (sum(kp.values()) * 1e-3) / 1e12
         log("[bench] packed layout kernels (ms): " + ", ".join(f"{n}={t:.3f}" for n, t in kp.items()))
+        credit_d = {"fwd": 4 * D * Pd, "bwd_dq": 2 * D * Pd, "bwd_dkdv": 8 * D * Pd}
         padded_info = {
             "seq_lens": sl.tolist(),
             "valid_pair_fraction": round(P / Pd, 4),
+            "per_kernel_padded_vs_dense": {
+                n: round((credit[n] / kt[n]) / (credit_d[n] / kd[n]), 4) for n in ("fwd", "bwd_dq", "bwd_dkdv")},
+            "dense_kernel_ms": {n: round(t, 4) for n, t in kd.items()},
             "padded_kernel_tflops": round(padded_tf, 2),
             "dense_kernel_tflops": round(dense_tf, 2),
             "padded_vs_dense": round(padded_tf / dense_tf, 4),

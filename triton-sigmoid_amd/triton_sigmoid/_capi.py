@@ -175,27 +175,41 @@ def _prepare(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k):
     for name, t in (("K", K), ("V", V)):
         if t.device != dev:
             raise RuntimeError(f"{name} is on {t.device}, expected {dev}")
-    bias = bias.to(device=dev, dtype=torch.float32).contiguous()
-    sm_scale = sm_scale.to(device=dev, dtype=torch.float32).reshape(()).contiguous()
-    if score_mod is not None:
-        score_mod = score_mod.to(device=dev, dtype=torch.float32).contiguous()
-    if seq_lens_q is not None:
-        seq_lens_q = seq_lens_q.to(device=dev, dtype=torch.int32).contiguous()
-    if seq_lens_k is not None:
-        seq_lens_k = seq_lens_k.to(device=dev, dtype=torch.int32).contiguous()
+    bias = _as(bias, torch.float32, dev)
+    sm_scale = _as(sm_scale, torch.float32, dev)
+    if sm_scale.dim() != 0:
+        sm_scale = sm_scale.reshape(())
+    score_mod = _as(score_mod, torch.float32, dev)
+    seq_lens_q = _as(seq_lens_q, torch.int32, dev)
+    seq_lens_k = _as(seq_lens_k, torch.int32, dev)
     return Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k
+
+
+def _as(t: Optional[torch.Tensor], dtype: torch.dtype, dev: torch.device) -> Optional[torch.Tensor]:
+    """t as a contiguous `dtype` tensor on `dev` (t itself when it already is)."""
+    if t is None or (t.dtype == dtype and t.device == dev and t.is_contiguous()):
+        return t
+    return t.to(device=dev, dtype=dtype).contiguous()
+
+
+def _on_device(dev: torch.device, fn):
+    """fn(stream) with `dev` current and torch's current HIP stream of it."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return fn(torch.cuda.current_stream().cuda_stream)
+    with torch.cuda.device(dev):
+        return fn(torch.cuda.current_stream(dev).cuda_stream)
 
 
 def _launch_fwd(lib, pr: SigattnProblem, out: torch.Tensor) -> None:
     """sigattn_fwd_ws with the workspace the problem asks for (decode shapes
     split their keys over several workgroups; others need none), allocated
     from torch's caching allocator on the output's device."""
-    with torch.cuda.device(out.device):
-        stream = torch.cuda.current_stream(out.device).cuda_stream
+    def run(stream):
         nbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=out.device) if nbytes else None
-        rc = lib.sigattn_fwd_ws(ctypes.byref(pr), out.data_ptr(), _ptr(ws), nbytes, stream)
-        _raise(rc, "sigattn_fwd")
+        _raise(lib.sigattn_fwd_ws(ctypes.byref(pr), out.data_ptr(), _ptr(ws), nbytes, stream), "sigattn_fwd")
+
+    _on_device(out.device, run)
 
 
 # Two-pass backward (dS stored by the dK/dV kernel, dQ = dS·K read back):
@@ -219,15 +233,15 @@ def bwd_workspace_limit() -> int:
 def _launch_bwd(lib, pr: SigattnProblem, dO, dQ, dK, dV) -> None:
     """sigattn_bwd_ws with a workspace from torch's caching allocator when
     the two-pass backward applies (see TWO_PASS_HEAD_DIMS), else sigattn_bwd."""
-    with torch.cuda.device(dQ.device):
-        stream = torch.cuda.current_stream(dQ.device).cuda_stream
+    def run(stream):
         nbytes = 0
         if pr.D in TWO_PASS_HEAD_DIMS:
             nbytes = min(int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))), bwd_workspace_limit())
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dQ.device) if nbytes else None
-        rc = lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
-                                stream)
-        _raise(rc, "sigattn_bwd_ws")
+        _raise(lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
+                                  stream), "sigattn_bwd_ws")
+
+    _on_device(dQ.device, run)
 
 
 def _raise(rc: int, what: str) -> None:
@@ -255,7 +269,7 @@ def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, cau
     lib = load_library()
     Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k = _prepare(
         Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
-    dO = dO.to(dtype=Q.dtype).contiguous()
+    dO = _as(dO, Q.dtype, Q.device)
     if dO.shape != Q.shape:
         raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
     dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
@@ -303,7 +317,7 @@ def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_s
     lib = load_library()
     Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
     cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
-    dO = dO.to(dtype=Q.dtype).contiguous()
+    dO = _as(dO, Q.dtype, Q.device)
     if dO.shape != Q.shape:
         raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
     dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
@@ -313,3 +327,31 @@ def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_s
                   packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
     _launch_bwd(lib, pr, dO, dQ, dK, dV)
     return dQ, dK, dV
+
+
+_CONSTANTS: dict = {}
+_CONSTANTS_MAX = 256
+
+
+def device_constant(shape, value, dtype: torch.dtype, device) -> torch.Tensor:
+    """A device tensor of `shape` filled with `value`, for the per-call bias /
+    scale / default-length tensors of the public APIs.  Eagerly the tensor is
+    made once per (shape, value, dtype, device) by a blocking host-to-device
+    copy (complete before first use on any stream) and reused, so a call
+    launches no fill kernels; under torch.compile it is an ordinary
+    torch.full in the graph, and under CUDA-graph capture a captured fill.
+    Callers never write to it."""
+    dev = torch.device(device)
+    if (torch.compiler.is_compiling() or dev.type != "cuda"
+            or torch.cuda.is_current_stream_capturing()):
+        return torch.full(shape, value, dtype=dtype, device=dev)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    key = (tuple(shape), float(value), dtype, dev)
+    t = _CONSTANTS.get(key)
+    if t is None:
+        if len(_CONSTANTS) >= _CONSTANTS_MAX:
+            _CONSTANTS.clear()
+        t = torch.full(shape, value, dtype=dtype).to(dev)
+        _CONSTANTS[key] = t
+    return t

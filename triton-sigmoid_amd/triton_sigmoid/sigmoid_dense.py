@@ -90,6 +90,29 @@ def _dense_backward(ctx, dO):
 sigmoid_attention_fwd_op.register_autograd(_dense_backward, setup_context=_dense_setup_context)
 
 
+class _DenseEager(torch.autograd.Function):
+    """Eager-mode path of sigmoid_attention: the same kernels, saved tensors
+    and gradients as myops::sigmoid_attention_fwd with its registered autograd,
+    without the custom-op dispatch (which costs more host time per call than
+    a small problem's kernels take).  torch.compile traces the registered op."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, bias, score_mod, sm_scale, is_causal):
+        out = _capi.forward(Q, K, V, bias, score_mod, sm_scale, None, None, is_causal)
+        _dense_setup_context(ctx, (Q, K, V, bias, score_mod, sm_scale, is_causal), out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dO):
+        if ctx.has_score_mod:
+            Q, K, V, bias, sm_scale, score_mod = ctx.saved_tensors
+        else:
+            Q, K, V, bias, sm_scale = ctx.saved_tensors
+            score_mod = None
+        dQ, dK, dV = _capi.backward(Q, K, V, dO, bias, score_mod, sm_scale, None, None, ctx.is_causal)
+        return dQ, dK, dV, None, None, None, None
+
+
 def sigmoid_attention(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -148,8 +171,9 @@ def sigmoid_attention(
         bias_value = float(sigmoid_bias)
     else:
         bias_value = -math.log(float(T)) if T > 0 else 0.0  # T == 0: nothing is computed
-    bias = torch.full((B,), bias_value, dtype=torch.float32, device=query.device)
+    bias = _capi.device_constant((B,), bias_value, torch.float32, query.device)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    scale_tensor = torch.full((), float(scale), dtype=torch.float32, device=query.device)
-    return sigmoid_attention_fwd_op(query, key, value, bias, score_mod, scale_tensor, is_causal)
+    scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
+    op = sigmoid_attention_fwd_op if torch.compiler.is_compiling() else _DenseEager.apply
+    return op(query, key, value, bias, score_mod, scale_tensor, is_causal)

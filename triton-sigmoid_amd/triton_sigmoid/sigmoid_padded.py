@@ -92,6 +92,28 @@ def _padded_backward(ctx, dO):
 sigmoid_attn_padded_fwd_op.register_autograd(_padded_backward, setup_context=_padded_setup_context)
 
 
+class _PaddedEager(torch.autograd.Function):
+    """Eager-mode path of sigmoid_attention_padded: the same kernels, saved
+    tensors and gradients as myops::sigmoid_attn_padded_fwd with its
+    registered autograd, without the custom-op dispatch.  torch.compile
+    traces the registered op."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, seq_lens_k, seq_lens_q, bias, score_mod, sm_scale, is_causal):
+        out = _capi.forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, is_causal)
+        _padded_setup_context(ctx, (Q, K, V, seq_lens_k, seq_lens_q, bias, score_mod, sm_scale, is_causal), out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dO):
+        saved = ctx.saved_tensors
+        Q, K, V, seq_lens_k, seq_lens_q, bias, sm_scale = saved[:7]
+        score_mod = saved[7] if ctx.has_score_mod else None
+        dQ, dK, dV = _capi.backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k,
+                                    ctx.is_causal)
+        return dQ, dK, dV, None, None, None, None, None, None
+
+
 def sigmoid_attention_padded(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -135,7 +157,7 @@ def sigmoid_attention_padded(
         raise ValueError(f"Key and value sequence lengths must match, got K={T_k}, V={T_v}")
 
     if seq_lens_k is None:
-        seq_lens_k = torch.full((B,), T_k, dtype=torch.int32, device=query.device)
+        seq_lens_k = _capi.device_constant((B,), T_k, torch.int32, query.device)
     else:
         if seq_lens_k.shape != (B,):
             raise ValueError(f"seq_lens_k must have shape ({B},), got {seq_lens_k.shape}")
@@ -144,7 +166,7 @@ def sigmoid_attention_padded(
         seq_lens_k = seq_lens_k.contiguous()
 
     if seq_lens_q is None:
-        seq_lens_q = torch.full((B,), T_q, dtype=torch.int32, device=query.device)
+        seq_lens_q = _capi.device_constant((B,), T_q, torch.int32, query.device)
     else:
         if seq_lens_q.shape != (B,):
             raise ValueError(f"seq_lens_q must have shape ({B},), got {seq_lens_q.shape}")
@@ -169,11 +191,10 @@ def sigmoid_attention_padded(
     if sigmoid_bias is None:
         bias = -torch.log(seq_lens_k.to(device=query.device, dtype=torch.float32))
     else:
-        bias = torch.full((B,), float(sigmoid_bias), dtype=torch.float32, device=query.device)
+        bias = _capi.device_constant((B,), float(sigmoid_bias), torch.float32, query.device)
 
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    scale_tensor = torch.full((), float(scale), dtype=torch.float32, device=query.device)
-    return sigmoid_attn_padded_fwd_op(
-        query, key, value, seq_lens_k, seq_lens_q, bias, score_mod, scale_tensor, is_causal
-    )
+    scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
+    op = sigmoid_attn_padded_fwd_op if torch.compiler.is_compiling() else _PaddedEager.apply
+    return op(query, key, value, seq_lens_k, seq_lens_q, bias, score_mod, scale_tensor, is_causal)

@@ -107,6 +107,31 @@ def _varlen_backward(ctx, dO):
 sigmoid_attn_varlen_fwd_op.register_autograd(_varlen_backward, setup_context=_varlen_setup_context)
 
 
+class _VarlenEager(torch.autograd.Function):
+    """Eager-mode path of sigmoid_attention_varlen: the same kernels, saved
+    tensors and gradients as myops::sigmoid_attn_varlen_fwd with its
+    registered autograd, without the custom-op dispatch.  torch.compile
+    traces the registered op."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, cu_seqlens_k, cu_seqlens_q, max_seqlen_k, max_seqlen_q, bias, score_mod, sm_scale,
+                is_causal):
+        out = _capi.forward_packed(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, bias,
+                                   score_mod, sm_scale, is_causal)
+        _varlen_setup_context(ctx, (Q, K, V, cu_seqlens_k, cu_seqlens_q, max_seqlen_k, max_seqlen_q, bias,
+                                    score_mod, sm_scale, is_causal), out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dO):
+        saved = ctx.saved_tensors
+        Q, K, V, cu_seqlens_k, cu_seqlens_q, bias, sm_scale = saved[:7]
+        score_mod = saved[7] if ctx.has_score_mod else None
+        dQ, dK, dV = _capi.backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, ctx.max_seqlen_q,
+                                           ctx.max_seqlen_k, bias, score_mod, sm_scale, ctx.is_causal)
+        return dQ, dK, dV, None, None, None, None, None, None, None, None
+
+
 def _check_cu(name: str, cu: torch.Tensor) -> torch.Tensor:
     if cu.dim() != 1 or cu.numel() < 1:
         raise ValueError(f"{name} must have shape (B + 1,), got {cu.shape}")
@@ -192,11 +217,10 @@ def sigmoid_attention_varlen(
     if sigmoid_bias is None:
         bias = -torch.log(lens_k.to(torch.float32))
     else:
-        bias = torch.full((B,), float(sigmoid_bias), dtype=torch.float32, device=query.device)
+        bias = _capi.device_constant((B,), float(sigmoid_bias), torch.float32, query.device)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    scale_tensor = torch.full((), float(scale), dtype=torch.float32, device=query.device)
-    return sigmoid_attn_varlen_fwd_op(
-        query, key, value, cu_seqlens_k.to(query.device), cu_seqlens_q.to(query.device),
-        int(max_seqlen_k), int(max_seqlen_q), bias, score_mod, scale_tensor, is_causal
-    )
+    scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
+    op = sigmoid_attn_varlen_fwd_op if torch.compiler.is_compiling() else _VarlenEager.apply
+    return op(query, key, value, cu_seqlens_k.to(query.device), cu_seqlens_q.to(query.device),
+              int(max_seqlen_k), int(max_seqlen_q), bias, score_mod, scale_tensor, is_causal)
