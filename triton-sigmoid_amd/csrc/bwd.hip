@@ -375,11 +375,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   auto store_ds = [&](int slot, int g) SIGATTN_INLINE {
     const int qb = mstart / 32 + g;
     const bool ok = g >= 0 && 32 * qb < Lq && kw < Lk && (!CAUSAL || qb >= kbw);
-    // Buffer over query block qb's tiles up to and including this wave's.
-    const uint16_t *row = ds_bh + DsLayout::tile(ok ? qb : 0, 0, p.ds_nkb, CAUSAL) * DsLayout::kTileElems;
+    // Buffer over this wave's tile (or over nothing).
+    const uint16_t *tp = ds_bh + (ok ? DsLayout::tile(qb, kbw, p.ds_nqb, CAUSAL) : 0) * DsLayout::kTileElems;
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, ok ? (kbw + 1) * 2048 : 0, kBufferWord3);
-    const int off = kbw * 2048 + 16 * lane;
+        __builtin_amdgcn_make_buffer_rsrc((void *)tp, (short)0, ok ? 2048 : 0, kBufferWord3);
+    const int off = 16 * lane;
     __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[slot][0], dw[slot][1], dw[slot][2], dw[slot][3]}, rs,
                                            off, 0, kStoreNT);
     __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[slot][4], dw[slot][5], dw[slot][6], dw[slot][7]}, rs,
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 // ---------------------------------------------------------------------------
 // dQ of the two-pass backward: dQ = dS · K · scale from the dS tiles the dK/dV
 // kernel stored (DsLayout), with no recomputation of S, P or dP.
-// Workgroup = 4 waves x 64 queries (two 32-query column blocks per wave);
+// Workgroup = NW waves x 64 queries (two 32-query column blocks per wave);
 // keys stream in stages of KB 32-key blocks through an NST-stage LDS ring:
 // the K rows (shared by the waves) and each wave's own dS tiles (its two
 // query blocks x KB key blocks), all by direct global->LDS copies issued
@@ -566,18 +566,18 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 // Per 32 keys a wave reads 4 KB of dS and runs 16 MFMAs: the kernel is bound
 // by HBM bandwidth.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL, int KB, int NST>
-__global__ __launch_bounds__(256, 1) void bwd_dq_ds_kernel(const KParams p) {
-  constexpr int BM = 256, BN = 32 * KB;
+template <typename T, int D, bool CAUSAL, int NW, int KB, int NST>
+__global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) {
+  constexpr int BM = 64 * NW, BN = 32 * KB;
   constexpr int NDB = D / 32;
   constexpr int TE = DsLayout::kTileElems;
-  constexpr int KI = BN * D / 8 / 64 / 4;  // K-row copy instructions per wave and stage
-  constexpr int NI = KI + 4 * KB;          // copy instructions per wave and stage
-  constexpr int PF = NST - 1;              // stages in flight ahead of the one computed
+  constexpr int KI = BN * D / 8 / 64 / NW;  // K-row copy instructions per wave and stage
+  constexpr int NI = KI + 4 * KB;           // copy instructions per wave and stage
+  constexpr int PF = NST - 1;               // stages in flight ahead of the one computed
   static_assert(KI >= 1 && (NST - 2) * NI < 64, "stage shape");
 
   __shared__ __attribute__((aligned(16))) uint16_t sK[NST][BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t sS[NST][4 * 2 * KB * TE];
+  __shared__ __attribute__((aligned(16))) uint16_t sS[NST][NW * 2 * KB * TE];
 
   int b, h, qblk;
   if (p.ragged() && p.B <= 64) {
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_ds_kernel(const KParams p) {
 
   TileOffsets<D> to;
   to.init(lane);
-  DmaPlan<BN, D, 4> dma;
+  DmaPlan<BN, D, NW> dma;
   dma.init(w, lane);
   const int kv_stride_bytes = (int)(p.sk_t * 2);
 
@@ -665,7 +665,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_ds_kernel(const KParams p) {
         const int qb = qbw + cb, kb = KB * u + kl;
         // Tiles the dK/dV pass did not store are replaced by tile 0 of this
         // (batch, head) (in bounds; their products are skipped).
-        const int64_t ti = tile_ok(qb, kb) ? DsLayout::tile(qb, kb, p.ds_nkb, CAUSAL) : 0;
+        const int64_t ti = tile_ok(qb, kb) ? DsLayout::tile(qb, kb, p.ds_nqb, CAUSAL) : 0;
         const uint16_t *src = ds_bh + ti * TE;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -785,11 +785,18 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
 
 template <typename T, int D>
 static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
-  launch_rows<256>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
-    // One 32-key block per stage in a 6-stage ring: 5 stages (about 120 KB per
-    // CU) in flight.
-    if (causal) bwd_dq_ds_kernel<T, D, true, 1, 6><<<grid, 256, 0, st>>>(p);
-    else bwd_dq_ds_kernel<T, D, false, 1, 6><<<grid, 256, 0, st>>>(p);
+  launch_rows<(D == 128 ? 512 : 256)>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+    // D = 128: 8 waves (512 query rows: each K row read serves twice the dS
+    // of a 4-wave workgroup; two waves per SIMD), one 32-key block per stage
+    // in a 3-stage ring.  D = 64: 4 waves (the K rows of a 32-key stage do not
+    // divide over 8 waves' copies), 6-stage ring.
+    if constexpr (D == 128) {
+      if (causal) bwd_dq_ds_kernel<T, D, true, 8, 1, 3><<<grid, 512, 0, st>>>(p);
+      else bwd_dq_ds_kernel<T, D, false, 8, 1, 3><<<grid, 512, 0, st>>>(p);
+    } else {
+      if (causal) bwd_dq_ds_kernel<T, D, true, 4, 1, 6><<<grid, 256, 0, st>>>(p);
+      else bwd_dq_ds_kernel<T, D, false, 4, 1, 6><<<grid, 256, 0, st>>>(p);
+    }
   });
 }
 

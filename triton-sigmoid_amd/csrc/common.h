@@ -213,9 +213,12 @@ struct WorkOrder {
 
 // ---------------------------------------------------------------------------
 // dS workspace of the two-pass backward.  dS of (batch, head) is cut into
-// 32-query x 32-key tiles of 2 KB.  Causal problems keep only the tiles that
-// hold a visible pair (key block <= query block), stored as a lower triangle
-// row by row; the others keep the full [query block][key block] rectangle.
+// 32-query x 32-key tiles of 2 KB, stored column by column (key block kb,
+// then query block qb), so the tiles one dQ workgroup reads for one key block
+// (its consecutive query blocks) are contiguous, and so are the tiles one
+// dK/dV wave writes for consecutive query blocks.  Causal problems keep only
+// the tiles that hold a visible pair (qb >= kb: column kb holds qb = kb ..
+// nqb-1); the others keep all nqb x nkb.
 // Inside a tile, lane l of the dK/dV kernel's accumulator layout (key l % 32,
 // query half h = l / 32) holds the 16-bit dS of queries {8g + 4h + i : g =
 // 0..3, i = 0..3}; piece c (g = 2c, 2c + 1, 16 bytes in (g, i) order) is
@@ -227,9 +230,11 @@ struct DsLayout {
   static __device__ __forceinline__ int64_t per_bh(int nqb, int nkb, bool causal) {
     return causal ? (int64_t)nqb * (nqb + 1) / 2 : (int64_t)nqb * nkb;
   }
-  // Tile index of (query block qb, key block kb) relative to the (b, h) base.
-  static __device__ __forceinline__ int64_t tile(int qb, int kb, int nkb, bool causal) {
-    return causal ? (int64_t)qb * (qb + 1) / 2 + kb : (int64_t)qb * nkb + kb;
+  // Tile index of (query block qb, key block kb) relative to the (b, h) base
+  // (causal: requires kb <= qb).
+  static __device__ __forceinline__ int64_t tile(int qb, int kb, int nqb, bool causal) {
+    const int64_t col = causal ? (int64_t)kb * nqb - (int64_t)kb * (kb - 1) / 2 : (int64_t)kb * nqb;
+    return col + (causal ? qb - kb : qb);
   }
 };
 
