@@ -9,6 +9,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 from triton_sigmoid import _capi
 
@@ -191,6 +192,33 @@ def test_two_pass_backward_workspace_size_and_errors():
     # null outputs are still reported first
     assert lib.sigattn_bwd_ws(ctypes.byref(p), fake, None, fake, fake, fake, nbytes, None) == -1
     assert lib.sigattn_bwd_dkdv_ws(ctypes.byref(p), None, fake, fake, fake, nbytes, None) == -1
+
+
+def test_python_layer_backward_workspace_policy(monkeypatch):
+    """The Python layer passes the whole dS when it fits the limit, else the
+    largest whole number of heads, and no workspace (the recompute backward)
+    at D != 128 or when one group's dQ-from-dS grid would have fewer
+    workgroups than the GPU has compute units."""
+    lib = _capi.load_library()
+    dev = torch.device("cuda", 0)
+    monkeypatch.setitem(_capi._CU_COUNT, 0, 256)
+    B, H, D, T = 2, 16, 128, 8192
+    p = _problem(B=B, H=H, Tq=T, Tk=T, D=D, q_stride_b=T * H * D, q_stride_t=H * D, q_stride_h=D,
+                 k_stride_b=T * H * D, k_stride_t=H * D, k_stride_h=D)
+    full = lib.sigattn_bwd_workspace_bytes(ctypes.byref(p))
+    per_head = full // H
+    assert per_head == B * 256 * 256 * 2048
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", str(full >> 20))
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == full
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "2303")   # 8 heads of 2 batches: 256 workgroups
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == 8 * per_head
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "2047")   # 7 heads: 224 workgroups
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == 0
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "0")
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == 0
+    monkeypatch.delenv("SIGATTN_BWD_WORKSPACE_MB")
+    p.D, p.q_stride_t, p.k_stride_t = 64, H * 64, H * 64
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == 0
 
 
 def test_empty_problems_return_before_any_launch():

@@ -230,13 +230,48 @@ def bwd_workspace_limit() -> int:
     return max(mb, 0) << 20
 
 
+# Query rows per workgroup of the D = 128 dQ-from-dS kernel.
+_DQ_DS_ROWS = 512
+_CU_COUNT: dict = {}
+
+
+def _compute_units(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNT.get(idx)
+    if n is None:
+        n = _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return n
+
+
+def bwd_workspace_bytes(lib, pr: SigattnProblem, device: torch.device) -> int:
+    """Workspace this layer gives sigattn_bwd_ws (0: the recompute backward).
+
+    The whole problem's dS when it fits bwd_workspace_limit(); otherwise the
+    largest whole number of heads that fits, run by the library one group
+    after another.  Groups whose dQ-from-dS grid has fewer workgroups than
+    the GPU has compute units are no faster than the recompute backward
+    (measured at D=128 non-causal: B=1 L=16384 H=16 in groups of 4 heads,
+    128 workgroups, 6.78 ms against 6.76 ms; B=2 L=8192 H=16 in groups of 8
+    heads, 256 workgroups, 3.14 ms against 3.44 ms), so those take it."""
+    if pr.D not in TWO_PASS_HEAD_DIMS:
+        return 0
+    full = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
+    limit = bwd_workspace_limit()
+    if full <= limit:
+        return full
+    per_head = full // pr.H
+    heads = limit // per_head
+    grid = heads * pr.B * -(-pr.Tq // _DQ_DS_ROWS)
+    if heads == 0 or grid < _compute_units(device):
+        return 0
+    return heads * per_head
+
+
 def _launch_bwd(lib, pr: SigattnProblem, dO, dQ, dK, dV) -> None:
     """sigattn_bwd_ws with a workspace from torch's caching allocator when
-    the two-pass backward applies (see TWO_PASS_HEAD_DIMS), else sigattn_bwd."""
+    the two-pass backward applies (bwd_workspace_bytes), else sigattn_bwd."""
     def run(stream):
-        nbytes = 0
-        if pr.D in TWO_PASS_HEAD_DIMS:
-            nbytes = min(int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))), bwd_workspace_limit())
+        nbytes = bwd_workspace_bytes(lib, pr, dQ.device)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dQ.device) if nbytes else None
         _raise(lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
                                   stream), "sigattn_bwd_ws")
