@@ -712,8 +712,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
     // A operand of MFMA m of the region whose blocks (S block, dV block) sit
     // at tile rows kl in ring stages stc / stg.
     auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
-      if (m < NKS) return ld_row<D>(sQ[stc], to, kl, m);
-      const int i = m - NKS;
+      if (m % 2 == 0) return ld_row<D>(sQ[stc], to, kl, m / 2);
+      const int i = m / 2;
       return ld_tr<D>(sO[stg], to, kl / 16 + i / NDB, i % NDB);
     };
     u32x4 opq[LA];
@@ -737,10 +737,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         }
         asm volatile("" ::"v"(opq[m % LA]));
         const u32x4 a = opq[m % LA];
-        if (m < NKS) {
-          sacc[SL] = Elem<T>::mfma(a, kf[m], m == 0 ? zero16() : sacc[SL]);
+        if (m % 2 == 0) {
+          sacc[SL] = Elem<T>::mfma(a, kf[m / 2], m == 0 ? zero16() : sacc[SL]);
         } else {
-          const int i = m - NKS, j = i / NDB, dbi = i % NDB;
+          const int i = m / 2, j = i / NDB, dbi = i % NDB;
           const u32x4 bp = (u32x4){pw[SL][4 * j], pw[SL][4 * j + 1], pw[SL][4 * j + 2], pw[SL][4 * j + 3]};
           dva[dbi] = Elem<T>::mfma(a, bp, dva[dbi]);
         }
@@ -835,8 +835,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
     };
 
     auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
-      if (m < NKS) return ld_row<D>(sO[stc], to, kl, m);
-      const int i = m - NKS;
+      if (m % 2 == 0) return ld_row<D>(sO[stc], to, kl, m / 2);
+      const int i = m / 2;
       return ld_tr<D>(sQ[stg], to, kl / 16 + i / NDB, i % NDB);
     };
     u32x4 opq[LA];
@@ -894,10 +894,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         }
         asm volatile("" ::"v"(opq[m % LA]));
         const u32x4 a = opq[m % LA];
-        if (m < NKS) {
-          pacc[SL] = Elem<T>::mfma(a, vf[m], m == 0 ? zero16() : pacc[SL]);
+        if (m % 2 == 0) {
+          pacc[SL] = Elem<T>::mfma(a, vf[m / 2], m == 0 ? zero16() : pacc[SL]);
         } else {
-          const int i = m - NKS, j = i / NDB, dbi = i % NDB;
+          const int i = m / 2, j = i / NDB, dbi = i % NDB;
           const u32x4 bd = (u32x4){dw[4 * j], dw[4 * j + 1], dw[4 * j + 2], dw[4 * j + 3]};
           dka[dbi] = Elem<T>::mfma(a, bd, dka[dbi]);
         }
