@@ -593,342 +593,354 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   // P of block g, for pair w: sP[g & 1][w], lane l's elements 4c..4c+3 at 256 c + 4 l.
   __shared__ __attribute__((aligned(16))) float sP[2][4][1024];
 
-  int b, h, kblk;
+  // Work: ragged batches take one key block per workgroup in WorkOrder's
+  // order.  Dense problems take key blocks j and nblk-1-j in sequence
+  // (grid = ceil(nblk/2) per (batch, head)): under the causal mask the two
+  // together cost the same for every j, so all workgroups are equal, and
+  // the grid has half as many workgroup starts.
+  int b, h, kblk0, nitems;
   if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lk, BN, p.nblk, false)
                                : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lk, BN, p.nblk, lq);
-    b = it.b, h = it.h, kblk = it.blk;
+    b = it.b, h = it.h, kblk0 = it.blk, nitems = 1;
   } else {
     const int BH = p.B * p.H;
     const int bh = blockIdx.x % BH;
-    kblk = blockIdx.x / BH;  // causal: low key blocks carry the most work and come first
+    kblk0 = blockIdx.x / BH;
+    nitems = p.nblk - 1 - kblk0 > kblk0 ? 2 : 1;
     b = bh / p.H, h = bh % p.H;
   }
-  const int Lq = p.len_q(b);
-  const int Lk = p.len_k(b);
+  for (int item = 0; item < nitems; ++item) {
+    const int kblk = item == 0 ? kblk0 : p.nblk - 1 - kblk0;
+    // The previous key block's last reads of the ring and of the P buffers
+    // precede this block's fills.
+    if (item > 0) __syncthreads();
+    const int Lq = p.len_q(b);
+    const int Lk = p.len_k(b);
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int pair = wv & 3;
-  const bool role_a = wv < 4;
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int k0 = kblk * BN, kw = k0 + pair * 32, my_k = kw + l32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pair = wv & 3;
+    const bool role_a = wv < 4;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int k0 = kblk * BN, kw = k0 + pair * 32, my_k = kw + l32;
 
-  const int64_t qoff = p.q_base(b, h);
-  const int64_t koff = p.k_base(b, h);
-  const uint16_t *Qb = (const uint16_t *)p.q + qoff;
-  const uint16_t *dOb = (const uint16_t *)p.dout + qoff;
+    const int64_t qoff = p.q_base(b, h);
+    const int64_t koff = p.k_base(b, h);
+    const uint16_t *Qb = (const uint16_t *)p.q + qoff;
+    const uint16_t *dOb = (const uint16_t *)p.dout + qoff;
 
-  // Causal: queries before the workgroup's first key see none of its keys.
-  const int mstart = CAUSAL ? (k0 / BMQ) * BMQ : 0;
-  const int mend = (k0 >= Lk) ? mstart : Lq;
-  const int ntiles = mend > mstart ? (mend - mstart + BMQ - 1) / BMQ : 0;
-  const int NB = 2 * ntiles;
+    // Causal: queries before the workgroup's first key see none of its keys.
+    const int mstart = CAUSAL ? (k0 / BMQ) * BMQ : 0;
+    const int mend = (k0 >= Lk) ? mstart : Lq;
+    const int ntiles = mend > mstart ? (mend - mstart + BMQ - 1) / BMQ : 0;
+    const int NB = 2 * ntiles;
 
-  const float scale = *p.scale;
-  const bool kok = my_k < Lk;
+    const float scale = *p.scale;
+    const bool kok = my_k < Lk;
 
-  TileOffsets<D> to;
-  to.init(lane);
-  Dma dma;
-  dma.init(pair, lane);
-  const int q_stride_bytes = (int)(p.sq_t * 2);
-  auto issue = [&](int st, int t) SIGATTN_INLINE {
-    dma.issue(sQ[st], Qb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
-    dma.issue(sO[st], dOb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
-  };
-
-  // Zeroes the packed words of block g whose query lies before the block
-  // range (pipeline fill; as unsigned such queries may also wrap to huge
-  // values), at or past seq_lens_q, or (causal) before the lane's key.
-  auto mask_words = [&](uint32_t(&wds)[8], int g) SIGATTN_INLINE {
-    int qbase = mstart + 32 * g;
-    asm volatile("" : "+s"(qbase));  // keeps this rare fix-up in its own branch
-    const unsigned lo = CAUSAL ? (unsigned)max(my_k, mstart) : (unsigned)mstart;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int i = 2 * e;
-      const unsigned q0 = (unsigned)(qbase + 8 * (i / 4) + 4 * hi + (i % 4));
-      const bool ok0 = q0 >= lo && q0 < (unsigned)Lq;
-      const bool ok1 = q0 + 1u >= lo && q0 + 1u < (unsigned)Lq;
-      wds[e] &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
-    }
-  };
-  auto needs_mask = [&](int g) SIGATTN_INLINE {
-    const int qb0 = mstart + 32 * g;
-    return g < 0 || qb0 + 32 > Lq || (CAUSAL && qb0 < kw + 31);
-  };
-
-  // Pipeline fill: the gradient products of blocks -2 and -1 read ring stage
-  // NST-1 (zeroed here; tile NST-1 arrives only in region 2) against zero
-  // words, and B's first dS reads the zeroed P buffer 0.
-  for (int i = tid; i < BMQ * D / 8; i += 512) {
-    *(u32x4 *)&sQ[NST - 1][8 * i] = zero4();
-    *(u32x4 *)&sO[NST - 1][8 * i] = zero4();
-  }
-  for (int i = tid; i < 2 * 4 * 1024 / 4; i += 512) *(u32x4 *)(&sP[0][0][0] + 4 * i) = zero4();
-  if (!role_a && ntiles > 0) {
-    issue(0, 0);
-    if (ntiles > 1) {
-      issue(1, 1);
-      wait_vm<NCP>();
-    } else {
-      wait_dma();
-    }
-  }
-  __syncthreads();
-
-  const int kmax = p.k_rows_out(Lk);
-  if (role_a) {
-    // ---------------- role A: S, P, dV ----------------
-    const float bias = p.bias[b];
-    const float nsl = -scale * kLog2e;
-    float nc = -bias * kLog2e;
-    if (SCOREMOD) nc = kok ? -(bias + p.score_mod[p.mod_base(b) + my_k]) * kLog2e : 0.0f;
-    u32x4 kf[NKS];
-    {
-      const uint16_t *kr = (const uint16_t *)p.k + koff + (int64_t)my_k * p.sk_t + 8 * hi;
-#pragma unroll
-      for (int s = 0; s < NKS; ++s) kf[s] = kok ? *(const u32x4 *)(kr + 16 * s) : zero4();
-    }
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(kf[s]));
-
-    f32x16 dva[NDB], sacc[2];
-    uint32_t pw[2][8];
-#pragma unroll
-    for (int d = 0; d < NDB; ++d) dva[d] = zero16();
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      sacc[x] = zero16();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pw[x][e] = 0u;
-    }
-    float *xb0 = &sP[0][pair][4 * lane];
-    float *xb1 = &sP[1][pair][4 * lane];
-
-    // A operand of MFMA m of the region whose blocks (S block, dV block) sit
-    // at tile rows kl in ring stages stc / stg.
-    auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
-      if (m % 2 == 0) return ld_row<D>(sQ[stc], to, kl, m / 2);
-      const int i = m / 2;
-      return ld_tr<D>(sO[stg], to, kl / 16 + i / NDB, i % NDB);
+    TileOffsets<D> to;
+    to.init(lane);
+    Dma dma;
+    dma.init(pair, lane);
+    const int q_stride_bytes = (int)(p.sq_t * 2);
+    auto issue = [&](int st, int t) SIGATTN_INLINE {
+      dma.issue(sQ[st], Qb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
+      dma.issue(sO[st], dOb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
     };
-    u32x4 opq[LA];
-#pragma unroll
-    for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
 
-    auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
-      constexpr int U = decltype(u_tag)::value;
-      constexpr int SL = U % 2;                  // parity of blocks r and r-2
-      constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
-      constexpr int STC = (U / 2) % NST, STG = ((U + 6) / 2) % NST;
-      constexpr int STCn = ((U + 1) / 2) % NST, STGn = ((U + 7) / 2) % NST;
-      float *xb = SL ? xb0 : xb1;                // P buffer of block r-1
-      float keep[2];
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        if (m == BAR) {
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-        }
-        asm volatile("" ::"v"(opq[m % LA]));
-        const u32x4 a = opq[m % LA];
-        if (m % 2 == 0) {
-          sacc[SL] = Elem<T>::mfma(a, kf[m / 2], m == 0 ? zero16() : sacc[SL]);
-        } else {
-          const int i = m / 2, j = i / NDB, dbi = i % NDB;
-          const u32x4 bp = (u32x4){pw[SL][4 * j], pw[SL][4 * j + 1], pw[SL][4 * j + 2], pw[SL][4 * j + 3]};
-          dva[dbi] = Elem<T>::mfma(a, bp, dva[dbi]);
-        }
-        if (m + LA < NM) opq[m % LA] = read_op(m + LA, STC, STG, KL);
-        else opq[m % LA] = read_op(m + LA - NM, STCn, STGn, KLn);
-        // P of block r-1: element pair m at MFMA position m, stored to LDS
-        // four elements at a time.
-        if (m < 8) {
-          float pr[2];
-#pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[1 - SL][2 * m + x], nsl, nc));
-            pr[x] = __builtin_amdgcn_rcpf(1.0f + ex);
-          }
-          pw[1 - SL][m] = Elem<T>::pack(pr[0], pr[1]);
-          if (m % 2 == 0) {
-            keep[0] = pr[0];
-            keep[1] = pr[1];
-          } else {
-            *(float4 *)(xb + 256 * (m / 2)) = make_float4(keep[0], keep[1], pr[0], pr[1]);
-          }
-        }
+    // Zeroes the packed words of block g whose query lies before the block
+    // range (pipeline fill; as unsigned such queries may also wrap to huge
+    // values), at or past seq_lens_q, or (causal) before the lane's key.
+    auto mask_words = [&](uint32_t(&wds)[8], int g) SIGATTN_INLINE {
+      int qbase = mstart + 32 * g;
+      asm volatile("" : "+s"(qbase));  // keeps this rare fix-up in its own branch
+      const unsigned lo = CAUSAL ? (unsigned)max(my_k, mstart) : (unsigned)mstart;
+  #pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 2 * e;
+        const unsigned q0 = (unsigned)(qbase + 8 * (i / 4) + 4 * hi + (i % 4));
+        const bool ok0 = q0 >= lo && q0 < (unsigned)Lq;
+        const bool ok1 = q0 + 1u >= lo && q0 + 1u < (unsigned)Lq;
+        wds[e] &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
       }
-      if (r == 0 || needs_mask(r - 1)) mask_words(pw[1 - SL], r - 1);
+    };
+    auto needs_mask = [&](int g) SIGATTN_INLINE {
+      const int qb0 = mstart + 32 * g;
+      return g < 0 || qb0 + 32 > Lq || (CAUSAL && qb0 < kw + 31);
     };
 
-    for (int r0 = 0; r0 < NB + 2; r0 += 8) {
-      region(r0 + 0, std::integral_constant<int, 0>{});
-      if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
-      if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
-      if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
-      if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
-      if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
-      if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
-      if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
+    // Pipeline fill: the gradient products of blocks -2 and -1 read ring stage
+    // NST-1 (zeroed here; tile NST-1 arrives only in region 2) against zero
+    // words, and B's first dS reads the zeroed P buffer 0.
+    for (int i = tid; i < BMQ * D / 8; i += 512) {
+      *(u32x4 *)&sQ[NST - 1][8 * i] = zero4();
+      *(u32x4 *)&sO[NST - 1][8 * i] = zero4();
     }
-
-    if (my_k < kmax) {
-      uint16_t *vr = (uint16_t *)p.dv + koff + (int64_t)my_k * p.sk_t;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          u32x2 ov;
-          ov.x = Elem<T>::pack(dva[db][4 * g], dva[db][4 * g + 1]);
-          ov.y = Elem<T>::pack(dva[db][4 * g + 2], dva[db][4 * g + 3]);
-          if (!kok) ov = (u32x2){0u, 0u};
-          *(u32x2 *)(vr + d0) = ov;
-        }
+    for (int i = tid; i < 2 * 4 * 1024 / 4; i += 512) *(u32x4 *)(&sP[0][0][0] + 4 * i) = zero4();
+    if (!role_a && ntiles > 0) {
+      issue(0, 0);
+      if (ntiles > 1) {
+        issue(1, 1);
+        wait_vm<NCP>();
+      } else {
+        wait_dma();
       }
     }
-  } else {
-    // ---------------- role B: dP, dS, dK, tile copies ----------------
-    u32x4 vf[NKS];
-    {
-      const uint16_t *vr = (const uint16_t *)p.v + koff + (int64_t)my_k * p.sk_t + 8 * hi;
-#pragma unroll
-      for (int s = 0; s < NKS; ++s) vf[s] = kok ? *(const u32x4 *)(vr + 16 * s) : zero4();
-    }
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(vf[s]));
+    __syncthreads();
 
-    f32x16 dka[NDB], pacc[2];
-    uint32_t dw[8];
-#pragma unroll
-    for (int d = 0; d < NDB; ++d) dka[d] = zero16();
-    pacc[0] = zero16();
-    pacc[1] = zero16();
-    const float *xb0 = &sP[0][pair][4 * lane];
-    const float *xb1 = &sP[1][pair][4 * lane];
-
-    // Two-pass backward: this wave's dS tile of block g (DsLayout), skipped
-    // (a store through an empty buffer resource, which the hardware drops)
-    // past seq_lens_q / seq_lens_k or wholly above the causal diagonal, so
-    // every region issues exactly two stores and the copy waits below use
-    // fixed counts.
-    const int kbw = kw / 32;
-    uint16_t *ds_bh = nullptr;
-    if constexpr (DSOUT)
-      ds_bh = p.ds + ((int64_t)b * p.H + h) * DsLayout::per_bh(p.ds_nqb, p.ds_nkb, CAUSAL) *
-                         DsLayout::kTileElems;
-    auto store_ds = [&](int g) SIGATTN_INLINE {
-      const int qb = mstart / 32 + g;
-      const bool ok = g >= 0 && 32 * qb < Lq && kw < Lk && (!CAUSAL || qb >= kbw);
-      const uint16_t *tp = ds_bh + (ok ? DsLayout::tile(qb, kbw, p.ds_nqb, CAUSAL) : 0) * DsLayout::kTileElems;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void *)tp, (short)0, ok ? 2048 : 0, kBufferWord3);
-      const int off = 16 * lane;
-      __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[0], dw[1], dw[2], dw[3]}, rs, off, 0, kStoreNT);
-      __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[4], dw[5], dw[6], dw[7]}, rs, off + 1024, 0, kStoreNT);
-    };
-
-    auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
-      if (m % 2 == 0) return ld_row<D>(sO[stc], to, kl, m / 2);
-      const int i = m / 2;
-      return ld_tr<D>(sQ[stg], to, kl / 16 + i / NDB, i % NDB);
-    };
-    u32x4 opq[LA];
-#pragma unroll
-    for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
-
-    auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
-      constexpr int U = decltype(u_tag)::value;
-      constexpr int SL = U % 2;
-      constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
-      constexpr int STC = (U / 2) % NST, STG = ((U + 6) / 2) % NST;
-      constexpr int STCn = ((U + 1) / 2) % NST, STGn = ((U + 7) / 2) % NST;
-      // dS of block r-2: P from A (stored in region r-1), dP from the
-      // accumulator block r-2 left in pacc[SL].
+    const int kmax = p.k_rows_out(Lk);
+    if (role_a) {
+      // ---------------- role A: S, P, dV ----------------
+      const float bias = p.bias[b];
+      const float nsl = -scale * kLog2e;
+      float nc = -bias * kLog2e;
+      if (SCOREMOD) nc = kok ? -(bias + p.score_mod[p.mod_base(b) + my_k]) * kLog2e : 0.0f;
+      u32x4 kf[NKS];
       {
-        const float *xb = SL ? xb1 : xb0;
-        float4 pv[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) pv[c] = *(const float4 *)(xb + 256 * c);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pr0 = (e % 2 == 0) ? pv[e / 2].x : pv[e / 2].z;
-          const float pr1 = (e % 2 == 0) ? pv[e / 2].y : pv[e / 2].w;
-          const float t0 = pr0 * pacc[SL][2 * e], t1 = pr1 * pacc[SL][2 * e + 1];
-          dw[e] = Elem<T>::pack(__builtin_fmaf(-pr0, t0, t0), __builtin_fmaf(-pr1, t1, t1));
-        }
-        if (r < 2 || needs_mask(r - 2)) mask_words(dw, r - 2);
-        if constexpr (DSOUT) store_ds(r - 2);
+        const uint16_t *kr = (const uint16_t *)p.k + koff + (int64_t)my_k * p.sk_t + 8 * hi;
+  #pragma unroll
+        for (int s = 0; s < NKS; ++s) kf[s] = kok ? *(const u32x4 *)(kr + 16 * s) : zero4();
       }
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        if (m == BAR) {
-          if constexpr (U % 2 == 1) {
-            // The next region starts tile t: wait for this wave's copies of
-            // it (younger: the dS stores since and tile t+1's copies).
-            const int t = (r + 1) / 2;
-            if (t < ntiles) {
-              const bool more = t + 1 < ntiles;
-              if constexpr (DSOUT) {
-                if (r == 1) { if (more) wait_vm<4 + NCP>(); else wait_vm<4>(); }
-                else { if (more) wait_vm<6 + NCP>(); else wait_vm<6>(); }
-              } else {
-                if (more) wait_vm<NCP>(); else wait_dma();
-              }
+  #pragma unroll
+      for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(kf[s]));
+
+      f32x16 dva[NDB], sacc[2];
+      uint32_t pw[2][8];
+  #pragma unroll
+      for (int d = 0; d < NDB; ++d) dva[d] = zero16();
+  #pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        sacc[x] = zero16();
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) pw[x][e] = 0u;
+      }
+      float *xb0 = &sP[0][pair][4 * lane];
+      float *xb1 = &sP[1][pair][4 * lane];
+
+      // A operand of MFMA m of the region whose blocks (S block, dV block) sit
+      // at tile rows kl in ring stages stc / stg.
+      auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
+        if (m % 2 == 0) return ld_row<D>(sQ[stc], to, kl, m / 2);
+        const int i = m / 2;
+        return ld_tr<D>(sO[stg], to, kl / 16 + i / NDB, i % NDB);
+      };
+      u32x4 opq[LA];
+  #pragma unroll
+      for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
+
+      auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
+        constexpr int U = decltype(u_tag)::value;
+        constexpr int SL = U % 2;                  // parity of blocks r and r-2
+        constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
+        constexpr int STC = (U / 2) % NST, STG = ((U + 6) / 2) % NST;
+        constexpr int STCn = ((U + 1) / 2) % NST, STGn = ((U + 7) / 2) % NST;
+        float *xb = SL ? xb0 : xb1;                // P buffer of block r-1
+        float keep[2];
+  #pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          if (m == BAR) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+          }
+          asm volatile("" ::"v"(opq[m % LA]));
+          const u32x4 a = opq[m % LA];
+          if (m % 2 == 0) {
+            sacc[SL] = Elem<T>::mfma(a, kf[m / 2], m == 0 ? zero16() : sacc[SL]);
+          } else {
+            const int i = m / 2, j = i / NDB, dbi = i % NDB;
+            const u32x4 bp = (u32x4){pw[SL][4 * j], pw[SL][4 * j + 1], pw[SL][4 * j + 2], pw[SL][4 * j + 3]};
+            dva[dbi] = Elem<T>::mfma(a, bp, dva[dbi]);
+          }
+          if (m + LA < NM) opq[m % LA] = read_op(m + LA, STC, STG, KL);
+          else opq[m % LA] = read_op(m + LA - NM, STCn, STGn, KLn);
+          // P of block r-1: element pair m at MFMA position m, stored to LDS
+          // four elements at a time.
+          if (m < 8) {
+            float pr[2];
+  #pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[1 - SL][2 * m + x], nsl, nc));
+              pr[x] = __builtin_amdgcn_rcpf(1.0f + ex);
+            }
+            pw[1 - SL][m] = Elem<T>::pack(pr[0], pr[1]);
+            if (m % 2 == 0) {
+              keep[0] = pr[0];
+              keep[1] = pr[1];
+            } else {
+              *(float4 *)(xb + 256 * (m / 2)) = make_float4(keep[0], keep[1], pr[0], pr[1]);
             }
           }
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-          if constexpr (U % 2 == 0) {
-            // Every wave has finished region r-1, the last to read the stage
-            // of tile r/2 - 2: refill it with tile r/2 + 2.
-            const int t = r / 2 + 2;
-            if (t < ntiles) issue((U / 2 + 2) % NST, t);
+        }
+        if (r == 0 || needs_mask(r - 1)) mask_words(pw[1 - SL], r - 1);
+      };
+
+      for (int r0 = 0; r0 < NB + 2; r0 += 8) {
+        region(r0 + 0, std::integral_constant<int, 0>{});
+        if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
+        if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
+        if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
+        if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
+        if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
+        if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
+        if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
+      }
+
+      if (my_k < kmax) {
+        uint16_t *vr = (uint16_t *)p.dv + koff + (int64_t)my_k * p.sk_t;
+  #pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+  #pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d0 = db * 32 + 8 * g + 4 * hi;
+            u32x2 ov;
+            ov.x = Elem<T>::pack(dva[db][4 * g], dva[db][4 * g + 1]);
+            ov.y = Elem<T>::pack(dva[db][4 * g + 2], dva[db][4 * g + 3]);
+            if (!kok) ov = (u32x2){0u, 0u};
+            *(u32x2 *)(vr + d0) = ov;
           }
         }
-        asm volatile("" ::"v"(opq[m % LA]));
-        const u32x4 a = opq[m % LA];
-        if (m % 2 == 0) {
-          pacc[SL] = Elem<T>::mfma(a, vf[m / 2], m == 0 ? zero16() : pacc[SL]);
-        } else {
-          const int i = m / 2, j = i / NDB, dbi = i % NDB;
-          const u32x4 bd = (u32x4){dw[4 * j], dw[4 * j + 1], dw[4 * j + 2], dw[4 * j + 3]};
-          dka[dbi] = Elem<T>::mfma(a, bd, dka[dbi]);
-        }
-        if (m + LA < NM) opq[m % LA] = read_op(m + LA, STC, STG, KL);
-        else opq[m % LA] = read_op(m + LA - NM, STCn, STGn, KLn);
       }
-    };
+    } else {
+      // ---------------- role B: dP, dS, dK, tile copies ----------------
+      u32x4 vf[NKS];
+      {
+        const uint16_t *vr = (const uint16_t *)p.v + koff + (int64_t)my_k * p.sk_t + 8 * hi;
+  #pragma unroll
+        for (int s = 0; s < NKS; ++s) vf[s] = kok ? *(const u32x4 *)(vr + 16 * s) : zero4();
+      }
+  #pragma unroll
+      for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(vf[s]));
 
-    for (int r0 = 0; r0 < NB + 2; r0 += 8) {
-      region(r0 + 0, std::integral_constant<int, 0>{});
-      if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
-      if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
-      if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
-      if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
-      if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
-      if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
-      if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
-    }
+      f32x16 dka[NDB], pacc[2];
+      uint32_t dw[8];
+  #pragma unroll
+      for (int d = 0; d < NDB; ++d) dka[d] = zero16();
+      pacc[0] = zero16();
+      pacc[1] = zero16();
+      const float *xb0 = &sP[0][pair][4 * lane];
+      const float *xb1 = &sP[1][pair][4 * lane];
 
-    if (my_k < kmax) {
-      uint16_t *kr = (uint16_t *)p.dk + koff + (int64_t)my_k * p.sk_t;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          u32x2 ok_;
-          ok_.x = Elem<T>::pack(dka[db][4 * g] * scale, dka[db][4 * g + 1] * scale);
-          ok_.y = Elem<T>::pack(dka[db][4 * g + 2] * scale, dka[db][4 * g + 3] * scale);
-          if (!kok) ok_ = (u32x2){0u, 0u};
-          *(u32x2 *)(kr + d0) = ok_;
+      // Two-pass backward: this wave's dS tile of block g (DsLayout), skipped
+      // (a store through an empty buffer resource, which the hardware drops)
+      // past seq_lens_q / seq_lens_k or wholly above the causal diagonal, so
+      // every region issues exactly two stores and the copy waits below use
+      // fixed counts.
+      const int kbw = kw / 32;
+      uint16_t *ds_bh = nullptr;
+      if constexpr (DSOUT)
+        ds_bh = p.ds + ((int64_t)b * p.H + h) * DsLayout::per_bh(p.ds_nqb, p.ds_nkb, CAUSAL) *
+                           DsLayout::kTileElems;
+      auto store_ds = [&](int g) SIGATTN_INLINE {
+        const int qb = mstart / 32 + g;
+        const bool ok = g >= 0 && 32 * qb < Lq && kw < Lk && (!CAUSAL || qb >= kbw);
+        const uint16_t *tp = ds_bh + (ok ? DsLayout::tile(qb, kbw, p.ds_nqb, CAUSAL) : 0) * DsLayout::kTileElems;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void *)tp, (short)0, ok ? 2048 : 0, kBufferWord3);
+        const int off = 16 * lane;
+        __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[0], dw[1], dw[2], dw[3]}, rs, off, 0, kStoreNT);
+        __builtin_amdgcn_raw_buffer_store_b128((u32x4){dw[4], dw[5], dw[6], dw[7]}, rs, off + 1024, 0, kStoreNT);
+      };
+
+      auto read_op = [&](int m, int stc, int stg, int kl) SIGATTN_INLINE {
+        if (m % 2 == 0) return ld_row<D>(sO[stc], to, kl, m / 2);
+        const int i = m / 2;
+        return ld_tr<D>(sQ[stg], to, kl / 16 + i / NDB, i % NDB);
+      };
+      u32x4 opq[LA];
+  #pragma unroll
+      for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
+
+      auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
+        constexpr int U = decltype(u_tag)::value;
+        constexpr int SL = U % 2;
+        constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
+        constexpr int STC = (U / 2) % NST, STG = ((U + 6) / 2) % NST;
+        constexpr int STCn = ((U + 1) / 2) % NST, STGn = ((U + 7) / 2) % NST;
+        // dS of block r-2: P from A (stored in region r-1), dP from the
+        // accumulator block r-2 left in pacc[SL].
+        {
+          const float *xb = SL ? xb1 : xb0;
+          float4 pv[4];
+  #pragma unroll
+          for (int c = 0; c < 4; ++c) pv[c] = *(const float4 *)(xb + 256 * c);
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pr0 = (e % 2 == 0) ? pv[e / 2].x : pv[e / 2].z;
+            const float pr1 = (e % 2 == 0) ? pv[e / 2].y : pv[e / 2].w;
+            const float t0 = pr0 * pacc[SL][2 * e], t1 = pr1 * pacc[SL][2 * e + 1];
+            dw[e] = Elem<T>::pack(__builtin_fmaf(-pr0, t0, t0), __builtin_fmaf(-pr1, t1, t1));
+          }
+          if (r < 2 || needs_mask(r - 2)) mask_words(dw, r - 2);
+          if constexpr (DSOUT) store_ds(r - 2);
+        }
+  #pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          if (m == BAR) {
+            if constexpr (U % 2 == 1) {
+              // The next region starts tile t: wait for this wave's copies of
+              // it (younger: the dS stores since and tile t+1's copies).
+              const int t = (r + 1) / 2;
+              if (t < ntiles) {
+                const bool more = t + 1 < ntiles;
+                if constexpr (DSOUT) {
+                  if (r == 1) { if (more) wait_vm<4 + NCP>(); else wait_vm<4>(); }
+                  else { if (more) wait_vm<6 + NCP>(); else wait_vm<6>(); }
+                } else {
+                  if (more) wait_vm<NCP>(); else wait_dma();
+                }
+              }
+            }
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if constexpr (U % 2 == 0) {
+              // Every wave has finished region r-1, the last to read the stage
+              // of tile r/2 - 2: refill it with tile r/2 + 2.
+              const int t = r / 2 + 2;
+              if (t < ntiles) issue((U / 2 + 2) % NST, t);
+            }
+          }
+          asm volatile("" ::"v"(opq[m % LA]));
+          const u32x4 a = opq[m % LA];
+          if (m % 2 == 0) {
+            pacc[SL] = Elem<T>::mfma(a, vf[m / 2], m == 0 ? zero16() : pacc[SL]);
+          } else {
+            const int i = m / 2, j = i / NDB, dbi = i % NDB;
+            const u32x4 bd = (u32x4){dw[4 * j], dw[4 * j + 1], dw[4 * j + 2], dw[4 * j + 3]};
+            dka[dbi] = Elem<T>::mfma(a, bd, dka[dbi]);
+          }
+          if (m + LA < NM) opq[m % LA] = read_op(m + LA, STC, STG, KL);
+          else opq[m % LA] = read_op(m + LA - NM, STCn, STGn, KLn);
+        }
+      };
+
+      for (int r0 = 0; r0 < NB + 2; r0 += 8) {
+        region(r0 + 0, std::integral_constant<int, 0>{});
+        if (r0 + 1 < NB + 2) region(r0 + 1, std::integral_constant<int, 1>{});
+        if (r0 + 2 < NB + 2) region(r0 + 2, std::integral_constant<int, 2>{});
+        if (r0 + 3 < NB + 2) region(r0 + 3, std::integral_constant<int, 3>{});
+        if (r0 + 4 < NB + 2) region(r0 + 4, std::integral_constant<int, 4>{});
+        if (r0 + 5 < NB + 2) region(r0 + 5, std::integral_constant<int, 5>{});
+        if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
+        if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
+      }
+
+      if (my_k < kmax) {
+        uint16_t *kr = (uint16_t *)p.dk + koff + (int64_t)my_k * p.sk_t;
+  #pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+  #pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d0 = db * 32 + 8 * g + 4 * hi;
+            u32x2 ok_;
+            ok_.x = Elem<T>::pack(dka[db][4 * g] * scale, dka[db][4 * g + 1] * scale);
+            ok_.y = Elem<T>::pack(dka[db][4 * g + 2] * scale, dka[db][4 * g + 3] * scale);
+            if (!kok) ok_ = (u32x2){0u, 0u};
+            *(u32x2 *)(kr + d0) = ok_;
+          }
         }
       }
     }
@@ -1161,6 +1173,8 @@ template <typename T, int D, bool DSOUT>
 static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   launch_rows<128>(kp, kp.Tk, [&](const KParams &p, dim3 grid) {
     if constexpr (D == 128) {
+      // Dense problems: two key blocks per workgroup (see the kernel).
+      if (!(p.ragged_host() && p.B <= 64)) grid = dim3((unsigned)(((p.nblk + 1) / 2) * p.B * p.H));
       if (causal) {
         if (sm) bwd_dkdv_pair_kernel<T, true, true, DSOUT><<<grid, 512, 0, st>>>(p);
         else bwd_dkdv_pair_kernel<T, true, false, DSOUT><<<grid, 512, 0, st>>>(p);

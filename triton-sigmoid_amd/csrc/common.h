@@ -119,6 +119,7 @@ struct KParams {
   __device__ __forceinline__ bool ragged() const {
     return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr;
   }
+  bool ragged_host() const { return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr; }
 };
 
 // ---------------------------------------------------------------------------
