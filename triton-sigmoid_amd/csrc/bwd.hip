@@ -552,11 +552,13 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 // dK/dV at D = 128 by wave pairs: workgroup = 8 waves, 128 keys.  Waves w and
 // w + 4 own the same 32 keys and share SIMD w (waves are dealt to the four
 // SIMDs round-robin), so each SIMD runs one wave of each role:
-//   role A (waves 0-3): S = Q·Kᵀ (K rows in registers), P = sigmoid(S) and
-//     dVᵀ += dOᵀ·P;
+//   role A (waves 0-3): S = Q·Kᵀ (K rows in registers), P = sigmoid(S),
+//     dVᵀ += dOᵀ·P, and every Q / dO tile copy;
 //   role B (waves 4-7): dP = dO·Vᵀ (V rows in registers), dS = P·(1-P)·dP,
-//     dKᵀ += Qᵀ·dS, the dS tiles of the two-pass backward, and every Q / dO
-//     tile copy.
+//     dKᵀ += Qᵀ·dS, and the dS tiles of the two-pass backward.
+// The copies and the stores sit in different waves because a wave's memory
+// operations complete in issue order: a copy wait behind dS stores would
+// also wait for their acknowledgement (measured 3-7 % of the kernel).
 // A hands P to B through LDS in fp32, so dS is computed from exactly the
 // values bwd_dkdv_kernel uses and dK, dV are bit for bit the same.  Either
 // role needs about half that kernel's registers (every accumulator stays in
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 //      dK of block r-2.
 // Every region has one barrier, placed before the operand read-ahead reaches
 // the next region's first MFMAs: it publishes the tile of the next region
-// (B waits for its copies just before) and the P that A stored before it,
+// (A waits for its copies just before) and the P that A stored before it,
 // which B reads in the next region (the two P buffers alternate by block
 // parity).
 // ---------------------------------------------------------------------------
@@ -680,7 +682,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
       *(u32x4 *)&sO[NST - 1][8 * i] = zero4();
     }
     for (int i = tid; i < 2 * 4 * 1024 / 4; i += 512) *(u32x4 *)(&sP[0][0][0] + 4 * i) = zero4();
-    if (!role_a && ntiles > 0) {
+    if (role_a && ntiles > 0) {
       issue(0, 0);
       if (ntiles > 1) {
         issue(1, 1);
@@ -742,9 +744,24 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   #pragma unroll
         for (int m = 0; m < NM; ++m) {
           if (m == BAR) {
+            if constexpr (U % 2 == 1) {
+              // The next region starts tile t: wait for this wave's copies
+              // of it (tile t+1's may stay in flight).
+              const int t = (r + 1) / 2;
+              if (t < ntiles) {
+                if (t + 1 < ntiles) wait_vm<NCP>();
+                else wait_dma();
+              }
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
+            if constexpr (U % 2 == 0) {
+              // Every wave has finished region r-1, the last to read the
+              // stage of tile r/2 - 2: refill it with tile r/2 + 2.
+              const int t = r / 2 + 2;
+              if (t < ntiles) issue((U / 2 + 2) % NST, t);
+            }
           }
           asm volatile("" ::"v"(opq[m % LA]));
           const u32x4 a = opq[m % LA];
@@ -826,9 +843,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
 
       // Two-pass backward: this wave's dS tile of block g (DsLayout), skipped
       // (a store through an empty buffer resource, which the hardware drops)
-      // past seq_lens_q / seq_lens_k or wholly above the causal diagonal, so
-      // every region issues exactly two stores and the copy waits below use
-      // fixed counts.
+      // past seq_lens_q / seq_lens_k or wholly above the causal diagonal.
       const int kbw = kw / 32;
       uint16_t *ds_bh = nullptr;
       if constexpr (DSOUT)
@@ -880,28 +895,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   #pragma unroll
         for (int m = 0; m < NM; ++m) {
           if (m == BAR) {
-            if constexpr (U % 2 == 1) {
-              // The next region starts tile t: wait for this wave's copies of
-              // it (younger: the dS stores since and tile t+1's copies).
-              const int t = (r + 1) / 2;
-              if (t < ntiles) {
-                const bool more = t + 1 < ntiles;
-                if constexpr (DSOUT) {
-                  if (r == 1) { if (more) wait_vm<4 + NCP>(); else wait_vm<4>(); }
-                  else { if (more) wait_vm<6 + NCP>(); else wait_vm<6>(); }
-                } else {
-                  if (more) wait_vm<NCP>(); else wait_dma();
-                }
-              }
-            }
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if constexpr (U % 2 == 0) {
-              // Every wave has finished region r-1, the last to read the stage
-              // of tile r/2 - 2: refill it with tile r/2 + 2.
-              const int t = r / 2 + 2;
-              if (t < ntiles) issue((U / 2 + 2) % NST, t);
-            }
           }
           asm volatile("" ::"v"(opq[m % LA]));
           const u32x4 a = opq[m % LA];
