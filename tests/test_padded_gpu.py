@@ -67,6 +67,36 @@ def test_padded_matches_oracle(dtype, D, Tq, Tk, causal):
         assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_many_batches_odd_key_blocks(causal):
+    """B > 64 takes the kernels' plain grid order, where the D = 128 dK/dV
+    kernel runs key blocks j and nblk-1-j in one workgroup; T = 300 gives an
+    odd number (3) of 128-key blocks, so one workgroup has a single block.
+    Lengths include 0 and the full T."""
+    B, T, H, D = 70, 300, 1, 128
+    dtype = torch.bfloat16
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=70 + int(causal), noise=False, lo=0.0)
+    sq[0], sq[1] = 0, T
+    sk.copy_(sq)
+    for b in range(B):  # padding rows hold NaN: they must never be read
+        for t in (q, k, v, do):
+            t[b, int(sq[b]):] = float("nan")
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal)
+    o.backward(do)
+    bias = (-torch.log(sk.float())).double().cpu().numpy()
+    qc, kc, vc, doc = _clean(q, sq), _clean(k, sk), _clean(v, sk), _clean(do, sq)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(qc, kc, vc, doc, scale=np.float32(1 / math.sqrt(D)), bias=bias,
+                                          seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+    for b in range(B):
+        assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("causal", [False, True])
 def test_padded_reference_criterion(dtype, causal):
