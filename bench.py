@@ -247,6 +247,29 @@ def copy_calibration(nbytes: int = 1 << 30) -> None:
     log(f"[bench] copy calibration: {nbytes} bytes read, {nbytes} bytes written")
 
 
+def mfma_ceiling(n: int = 8192, iters: int = 20):
+    """Practical MFMA rate of this GPU: hipBLASLt's bf16 GEMM (torch.matmul,
+    n x n x n, fp32 accumulation) on N(0,1) operands and on all-zero
+    operands.  The chip's power limit lowers the clock with data activity, so
+    the random-operand rate is the ceiling a dense bf16 kernel can reach on
+    this box; the zero-operand rate shows how far the spec clock is from it."""
+    import torch
+    g = torch.Generator().manual_seed(0)
+    out = {}
+    for name in ("random", "zero"):
+        a = torch.randn((n, n), generator=g).to(torch.bfloat16).cuda()
+        b = torch.randn((n, n), generator=g).to(torch.bfloat16).cuda()
+        if name == "zero":
+            a.zero_()
+            b.zero_()
+        ms, _ = time_region(lambda: torch.matmul(a, b), iters, 5)
+        out[name] = {"ms": round(ms, 4), "tflops": round(2 * n ** 3 / ms / 1e9, 1)}
+        del a, b
+    return {"gemm": f"torch.matmul bf16 {n}x{n}x{n}", "peak_tflops": PEAK_BF16_TFLOPS,
+            "random_operands": out["random"], "zero_operands": out["zero"],
+            "random_frac_of_peak": round(out["random"]["tflops"] / PEAK_BF16_TFLOPS, 4)}
+
+
 def load_traffic(kernel: str, config: str):
     """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc FETCH_SIZE
     and WRITE_SIZE (scaled by the copy calibration), from profiles/hbm_traffic.json."""
@@ -411,7 +434,13 @@ def main():
                     help="the reference benchmark's L/D/padding grid, beside its published H100 chart")
     ap.add_argument("--decode", action="store_true",
                     help="split-KV forward at decode shapes (HBM GB/s)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="hipBLASLt bf16 GEMM TFLOPS on random and on zero operands (the box's practical MFMA rate)")
     args = ap.parse_args()
+    if args.ceiling:
+        print(json.dumps({"metric": "practical MFMA rate (bf16 GEMM)", "unit": "TFLOPS", **mfma_ceiling()}),
+              flush=True)
+        return
     if args.copy_calibration:
         copy_calibration()
         return
