@@ -44,6 +44,28 @@ def test_dense_matches_oracle(dtype, D, T, causal):
     assert_close_to_oracle(v.grad, dv, dtype, "dV")
 
 
+@pytest.mark.parametrize("H", [1, 5, 12])
+@pytest.mark.parametrize("D", [64, 128])
+def test_various_num_heads_match_oracle(H, D):
+    """Head counts that do not divide any tile (the reference's
+    tests/test_sigmoid_dense.py:621-637 checks shape and NaN only)."""
+    B, T = 2, 200
+    dtype = torch.bfloat16
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=H * 31 + D)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=True)
+    o.backward(do)
+    bias = np.full(B, -math.log(T), dtype=np.float32).astype(np.float64)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1.0 / math.sqrt(D)), bias=bias,
+                                          causal=True)
+    assert o.shape == (B, T, H, D)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])

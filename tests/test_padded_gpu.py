@@ -67,6 +67,52 @@ def test_padded_matches_oracle(dtype, D, Tq, Tk, causal):
         assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
 
 
+def _padded_vs_oracle(q, k, v, do, sq, sk, causal, dtype):
+    """Runs sigmoid_attention_padded forward + backward and checks O and the
+    gradients against the oracle on the inputs with padding rows zeroed."""
+    D = q.shape[-1]
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal)
+    o.backward(do)
+    Lq = sq if sq is not None else torch.full((q.shape[0],), q.shape[1], dtype=torch.int32)
+    bias = (-torch.log(sk.float())).double().cpu().numpy()
+    qc, kc, vc, doc = _clean(q, Lq), _clean(k, sk), _clean(v, sk), _clean(do, Lq)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(qc, kc, vc, doc, scale=np.float32(1 / math.sqrt(D)), bias=bias,
+                                          seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_extreme_length_variation(D, causal):
+    """Key lengths from 16 to the full T in one batch, queries unpadded (the
+    reference's tests/test_sigmoid_padded.py:752-773 checks NaN only)."""
+    B, T, H = 4, 256, 3
+    dtype = torch.float16
+    q, k, v, do, _, _ = _case(B, T, T, H, D, dtype, seed=D + int(causal), noise=False)
+    sk = torch.tensor([16, 64, 128, T], dtype=torch.int32, device=DEV)
+    for b in range(B):  # padding keys hold NaN: they must never be read
+        k[b, int(sk[b]):] = float("nan")
+        v[b, int(sk[b]):] = float("nan")
+    _padded_vs_oracle(q, k, v, do, None, sk, causal, dtype)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Tq,Tk", [(32, 512), (512, 32), (1, 2048), (2048, 1)])
+def test_cross_attention_extreme_length_ratio(D, Tq, Tk):
+    """Very different query and key lengths, both padded (the reference's
+    tests/test_sigmoid_padded.py:776-798 checks NaN only).  Tq = 1 against
+    2048 keys takes the split-KV decode kernel."""
+    B, H = 2, 2
+    dtype = torch.bfloat16
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=Tq + Tk + D)
+    _padded_vs_oracle(q, k, v, do, sq, sk, False, dtype)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_padded_many_batches_odd_key_blocks(causal):
     """B > 64 takes the kernels' plain grid order, where the D = 128 dK/dV
