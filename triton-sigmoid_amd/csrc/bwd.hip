@@ -587,7 +587,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   constexpr int LA = 4;                   // operand read-ahead, in MFMAs
   constexpr int BAR = NM - LA;            // MFMA position of the region's barrier
   using Dma = DmaPlan<BMQ, D, 4>;
-  constexpr int NCP = 2 * Dma::NI;        // copy instructions per tile and B wave
+  constexpr int NCP = 2 * Dma::NI;        // copy instructions per tile and A wave
   static_assert(NM % LA == 0 && BAR >= 8, "region shape");
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[NST][BMQ * D];
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
       int qbase = mstart + 32 * g;
       asm volatile("" : "+s"(qbase));  // keeps this rare fix-up in its own branch
       const unsigned lo = CAUSAL ? (unsigned)max(my_k, mstart) : (unsigned)mstart;
-  #pragma unroll
+#pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = 2 * e;
         const unsigned q0 = (unsigned)(qbase + 8 * (i / 4) + 4 * hi + (i % 4));
@@ -703,20 +703,20 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
       u32x4 kf[NKS];
       {
         const uint16_t *kr = (const uint16_t *)p.k + koff + (int64_t)my_k * p.sk_t + 8 * hi;
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < NKS; ++s) kf[s] = kok ? *(const u32x4 *)(kr + 16 * s) : zero4();
       }
-  #pragma unroll
+#pragma unroll
       for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(kf[s]));
 
       f32x16 dva[NDB], sacc[2];
       uint32_t pw[2][8];
-  #pragma unroll
+#pragma unroll
       for (int d = 0; d < NDB; ++d) dva[d] = zero16();
-  #pragma unroll
+#pragma unroll
       for (int x = 0; x < 2; ++x) {
         sacc[x] = zero16();
-  #pragma unroll
+#pragma unroll
         for (int e = 0; e < 8; ++e) pw[x][e] = 0u;
       }
       float *xb0 = &sP[0][pair][4 * lane];
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         return ld_tr<D>(sO[stg], to, kl / 16 + i / NDB, i % NDB);
       };
       u32x4 opq[LA];
-  #pragma unroll
+#pragma unroll
       for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
 
       auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         constexpr int STCn = ((U + 1) / 2) % NST, STGn = ((U + 7) / 2) % NST;
         float *xb = SL ? xb0 : xb1;                // P buffer of block r-1
         float keep[2];
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < NM; ++m) {
           if (m == BAR) {
             if constexpr (U % 2 == 1) {
@@ -778,7 +778,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
           // four elements at a time.
           if (m < 8) {
             float pr[2];
-  #pragma unroll
+#pragma unroll
             for (int x = 0; x < 2; ++x) {
               const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[1 - SL][2 * m + x], nsl, nc));
               pr[x] = __builtin_amdgcn_rcpf(1.0f + ex);
@@ -808,9 +808,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
 
       if (my_k < kmax) {
         uint16_t *vr = (uint16_t *)p.dv + koff + (int64_t)my_k * p.sk_t;
-  #pragma unroll
+#pragma unroll
         for (int db = 0; db < NDB; ++db) {
-  #pragma unroll
+#pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int d0 = db * 32 + 8 * g + 4 * hi;
             u32x2 ov;
@@ -826,15 +826,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
       u32x4 vf[NKS];
       {
         const uint16_t *vr = (const uint16_t *)p.v + koff + (int64_t)my_k * p.sk_t + 8 * hi;
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < NKS; ++s) vf[s] = kok ? *(const u32x4 *)(vr + 16 * s) : zero4();
       }
-  #pragma unroll
+#pragma unroll
       for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(vf[s]));
 
       f32x16 dka[NDB], pacc[2];
       uint32_t dw[8];
-  #pragma unroll
+#pragma unroll
       for (int d = 0; d < NDB; ++d) dka[d] = zero16();
       pacc[0] = zero16();
       pacc[1] = zero16();
@@ -866,7 +866,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         return ld_tr<D>(sQ[stg], to, kl / 16 + i / NDB, i % NDB);
       };
       u32x4 opq[LA];
-  #pragma unroll
+#pragma unroll
       for (int m = 0; m < LA; ++m) opq[m] = read_op(m, 0, NST - 1, 0);
 
       auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
@@ -880,9 +880,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         {
           const float *xb = SL ? xb1 : xb0;
           float4 pv[4];
-  #pragma unroll
+#pragma unroll
           for (int c = 0; c < 4; ++c) pv[c] = *(const float4 *)(xb + 256 * c);
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float pr0 = (e % 2 == 0) ? pv[e / 2].x : pv[e / 2].z;
             const float pr1 = (e % 2 == 0) ? pv[e / 2].y : pv[e / 2].w;
@@ -892,7 +892,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
           if (r < 2 || needs_mask(r - 2)) mask_words(dw, r - 2);
           if constexpr (DSOUT) store_ds(r - 2);
         }
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < NM; ++m) {
           if (m == BAR) {
             __builtin_amdgcn_s_barrier();
@@ -925,9 +925,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
 
       if (my_k < kmax) {
         uint16_t *kr = (uint16_t *)p.dk + koff + (int64_t)my_k * p.sk_t;
-  #pragma unroll
+#pragma unroll
         for (int db = 0; db < NDB; ++db) {
-  #pragma unroll
+#pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int d0 = db * 32 + 8 * g + 4 * hi;
             u32x2 ok_;
