@@ -242,6 +242,9 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   constexpr int PPW = 8 / NWIN;           // element pairs per window
   constexpr int BAR = NM - LA;            // MFMA position of the tile barrier in odd regions
   static_assert(NM % LA == 0 && BAR % 4 == 0, "region shape");
+  // The region loop unrolls 8 regions (4 tiles); its compile-time stage
+  // indices need 4 tiles to be a whole number of ring turns.
+  static_assert(4 % NST == 0, "ring stages");
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[NST][BMQ * D];
   __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];
@@ -589,6 +592,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   using Dma = DmaPlan<BMQ, D, 4>;
   constexpr int NCP = 2 * Dma::NI;        // copy instructions per tile and A wave
   static_assert(NM % LA == 0 && BAR >= 8, "region shape");
+  // The region loop unrolls 8 regions (4 tiles); its compile-time stage
+  // indices need 4 tiles to be a whole number of ring turns.
+  static_assert(4 % NST == 0, "ring stages");
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[NST][BMQ * D];
   __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace sigattn {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -311,6 +313,16 @@ __device__ __forceinline__ uint32_t gather2(const u32x4 &r0, const u32x4 &r1, in
 }
 
 __device__ __forceinline__ u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
+
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1 in order, inlined.
+template <int B, int E> struct Unroll {
+  template <class F> static __device__ __forceinline__ void run(F &&f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      Unroll<B + 1, E>::run(f);
+    }
+  }
+};
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;

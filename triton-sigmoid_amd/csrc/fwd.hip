@@ -33,12 +33,13 @@
 namespace sigattn {
 
 template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) {
+__global__ __launch_bounds__(64 * NWV, (D == 64 ? 3 : 1)) void fwd_mfma_kernel(const KParams p) {
   // NWV waves per workgroup (8: two per SIMD), NCB 32-query column blocks each.
   constexpr int QW = 32 * NCB;          // queries per wave
   constexpr int BM = NWV * QW;          // queries per workgroup
   constexpr int BN = 64;                // keys per LDS tile (two 32-key blocks)
-  constexpr int NST = 4;                // LDS ring stages
+  // LDS ring stages: D = 64 uses three (48 KB), so three workgroups share a CU.
+  constexpr int NST = D == 64 ? 3 : 4;
   constexpr int NKS = D / 16;           // MFMA k-steps over the head dim
   constexpr int NDB = D / 32;           // 32-row blocks of Oᵀ
   constexpr int NSTEP = NKS + 2 * NDB;  // steps (NCB MFMAs sharing an A operand) per region
@@ -186,16 +187,18 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   // Block g lives in tile g/2 (rows 32*(g%2)) in ring stage (g/2)%4.  In odd
   // regions r = 2u-1, step BAR publishes tile u (its first read, the K rows of
   // block r+1, comes next) and starts the copy of tile u+1 into the stage of
-  // tile u-3, whose last reads were issued two regions earlier -- so the
-  // barrier needs no wait for this wave's own in-flight LDS reads.
+  // tile u+1-NST.  With four stages that tile's last reads were issued two
+  // regions earlier, so the barrier needs no wait for this wave's own LDS
+  // reads; with three (D = 64) they were issued in this region, and every
+  // wave waits for them before the barrier.
   auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
     constexpr int U = decltype(u_tag)::value;
     constexpr int SL = U % 2;                    // parity of blocks r and r-2
     constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
     constexpr int STC = (U / 2) % NST;           // stage of block r
-    constexpr int STV = ((U + 6) / 2) % NST;     // stage of block r-2
+    constexpr int STV = ((U + 2 * NST - 2) / 2) % NST;  // stage of block r-2
     constexpr int STCn = ((U + 1) / 2) % NST;    // stage of block r+1
-    constexpr int STVn = ((U + 7) / 2) % NST;    // stage of block r-1
+    constexpr int STVn = ((U + 2 * NST - 1) / 2) % NST;  // stage of block r-1
     f32x16(&sc)[NCB] = sbuf[SL];
     const f32x16(&sp)[NCB] = sbuf[1 - SL];
     uint32_t(&pn)[NCB][8] = pbuf[1 - SL];
@@ -222,6 +225,9 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
         if (u < ntiles) {
           wait_dma();
           if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
+          // With three stages the copy below refills the stage this region's
+          // Vᵀ operands came from: every wave's reads of it complete first.
+          if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           asm volatile("" ::: "memory");
           __builtin_amdgcn_s_barrier();
           asm volatile("" ::: "memory");
@@ -277,8 +283,9 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   };
 
   // Pipeline fill: Pᵀ(-2) = Pᵀ(-1) = 0 (the latter through its mask).  The
-  // Vᵀ operands of blocks -2 and -1 come from ring stage 3, zeroed here
-  // (tile 3 arrives only after region 5), so 0 * operand stays 0.
+  // Vᵀ operands of blocks -2 and -1 come from ring stage NST-1, zeroed here
+  // (tile NST-1 is copied into it from the barrier of region 2·NST-5 on,
+  // after every read of blocks -2 and -1), so 0 * operand stays 0.
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
@@ -308,15 +315,13 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
   if (CAUSAL) NBw = min(NBw, (qw + QW - 1) / 32 + 1);
   if (qw >= Lq) NBw = 0;
   const int RW = NBw > 0 ? NBw + 2 : 0;
-  for (int r0 = 0; r0 < RW; r0 += 8) {
-    region(r0 + 0, std::integral_constant<int, 0>{});
-    if (r0 + 1 < RW) region(r0 + 1, std::integral_constant<int, 1>{});
-    if (r0 + 2 < RW) region(r0 + 2, std::integral_constant<int, 2>{});
-    if (r0 + 3 < RW) region(r0 + 3, std::integral_constant<int, 3>{});
-    if (r0 + 4 < RW) region(r0 + 4, std::integral_constant<int, 4>{});
-    if (r0 + 5 < RW) region(r0 + 5, std::integral_constant<int, 5>{});
-    if (r0 + 6 < RW) region(r0 + 6, std::integral_constant<int, 6>{});
-    if (r0 + 7 < RW) region(r0 + 7, std::integral_constant<int, 7>{});
+  // One pass of the loop covers 2·NST regions (NST tiles), so region r0 + U
+  // starts tile r0/2 + U/2 with r0/2 a multiple of NST: every stage index in
+  // region() is a compile-time function of U.
+  for (int r0 = 0; r0 < RW; r0 += 2 * NST) {
+    Unroll<0, 2 * NST>::run([&](auto u) SIGATTN_INLINE {
+      if (r0 + decltype(u)::value < RW) region(r0 + decltype(u)::value, u);
+    });
   }
   // The rest of the workgroup's regions: the same barriers and copies.
   for (int r = RW | 1; r < NB + 2; r += 2) {
@@ -324,6 +329,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void fwd_mfma_kernel(const KParams p) 
     if (u < ntiles) {
       wait_dma();
       if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
+      if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
@@ -378,10 +384,12 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
   }
 }
 
-// D = 128: one workgroup of eight waves per CU (128 KB of LDS).  D = 64: the
-// ring takes 64 KB, so two workgroups of four waves share a CU -- the same two
-// waves per SIMD in half-size work units, which balance better on small or
-// ragged (padded) batches.
+// D = 128: one workgroup of eight waves per CU (128 KB of LDS).  D = 64: a
+// 3-stage ring of 48 KB, so three workgroups of four waves share a CU (three
+// waves per SIMD, at most 168 VGPRs each) in small work units, which balance
+// better on small or ragged (padded) batches.  Measured against two
+// workgroups per CU with a 4-stage ring: 10-20 % faster dense (c4, c5 shapes)
+// and 5-13 % padded.
 template <typename T, int D>
 static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
   launch_fwd_w<T, D, (D == 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
