@@ -185,18 +185,24 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         calls["bwd_dq"] = lambda: lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream)
         calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
                                                          dv.data_ptr(), stream)
+    # Median of three timed runs of `iters` launches each: the first kernel
+    # timed after a long step loop can read 10-20 % slow on its own.
     out = {}
     for name, fn in calls.items():
         for _ in range(3):
             assert fn() == 0
         torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(iters):
-            fn()
-        e.record()
-        e.synchronize()
-        out[name] = s.elapsed_time(e) / iters
+        runs = []
+        for _ in range(3):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                fn()
+            e.record()
+            e.synchronize()
+            runs.append(s.elapsed_time(e) / iters)
+        out[name] = statistics.median(runs)
+        log(f"[bench] kernel {name}: runs {', '.join(f'{r:.4f}' for r in runs)} ms")
     if nbytes:
         log(f"[bench] two-pass backward: dS workspace {nbytes / 1e9:.3f} GB; dQ-from-dS reads it at "
             f"{nbytes / (out['bwd_dq'] * 1e-3) / 1e12:.2f} TB/s")
