@@ -167,7 +167,7 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     # The forward the public API runs: with the workspace the library asks
-    # for (split-KV decode, or the split forward of ragged problems).
+    # for (the split-KV kernel at decode shapes; none otherwise).
     fbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
     fws = torch.empty(max(fbytes, 16), dtype=torch.uint8, device=q.device)
     calls = {"fwd": lambda: lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), fws.data_ptr() if fbytes else None,

@@ -1175,7 +1175,7 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
   launch_rows<128>(kp, kp.Tk, [&](const KParams &p, dim3 grid) {
     if constexpr (D == 128) {
       // Dense problems: two key blocks per workgroup (see the kernel).
-      if (!(p.ragged_host() && p.B <= 64)) grid = dim3((unsigned)(((p.nblk + 1) / 2) * p.B * p.H));
+      if (!(p.ragged() && p.B <= 64)) grid = dim3((unsigned)(((p.nblk + 1) / 2) * p.B * p.H));
       if (causal) {
         if (sm) bwd_dkdv_pair_kernel<T, true, true, DSOUT><<<grid, 512, 0, st>>>(p);
         else bwd_dkdv_pair_kernel<T, true, false, DSOUT><<<grid, 512, 0, st>>>(p);

@@ -118,10 +118,9 @@ struct KParams {
   __device__ __forceinline__ int q_rows_out(int Lq) const { return cu_q != nullptr ? Lq : Tq; }
   __device__ __forceinline__ int k_rows_out(int Lk) const { return cu_k != nullptr ? Lk : Tk; }
   // Batches differ in length (the work order then follows the lengths).
-  __device__ __forceinline__ bool ragged() const {
+  __host__ __device__ __forceinline__ bool ragged() const {
     return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr;
   }
-  bool ragged_host() const { return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr; }
 };
 
 // ---------------------------------------------------------------------------
