@@ -21,10 +21,13 @@ def _qkv(B, T, H, D, dtype, seed, Tk=None):
             randn((B, Tk, H, D), dtype, DEV, g), randn((B, T, H, D), dtype, DEV, g))
 
 
+@pytest.mark.parametrize("D,dtype", [(64, torch.float16), (128, torch.bfloat16)])
 @pytest.mark.parametrize("causal", [False, True])
-def test_compiled_dense_matches_eager(causal):
+def test_compiled_dense_matches_eager(causal, D, dtype):
+    """D = 128 takes the two-pass backward (dS workspace allocated inside the
+    compiled op), D = 64 the recompute backward."""
     torch._dynamo.reset()
-    q, k, v, do = _qkv(2, 256, 4, 64, torch.float16, 1)
+    q, k, v, do = _qkv(2, 256, 4, D, dtype, 1)
     f = torch.compile(ts.sigmoid_attention, fullgraph=True)
     leaves_e = [t.clone().requires_grad_(True) for t in (q, k, v)]
     leaves_c = [t.clone().requires_grad_(True) for t in (q, k, v)]
