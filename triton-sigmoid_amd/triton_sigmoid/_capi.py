@@ -120,7 +120,7 @@ def _check_device(t: torch.Tensor) -> None:
             "sigmoid attention kernels need tensors on an AMD gfx950 (MI355X) GPU under "
             f"PyTorch-ROCm; got a tensor on '{t.device}'"
         )
-    idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    idx = t.device.index if t.device.index is not None else torch._C._cuda_getDevice()
     if idx in _checked_devices:
         return
     arch = torch.cuda.get_device_properties(idx).gcnArchName.split(":")[0]
@@ -193,11 +193,17 @@ def _as(t: Optional[torch.Tensor], dtype: torch.dtype, dev: torch.device) -> Opt
 
 
 def _on_device(dev: torch.device, fn):
-    """fn(stream) with `dev` current and torch's current HIP stream of it."""
-    if dev.index is None or dev.index == torch.cuda.current_device():
-        return fn(torch.cuda.current_stream().cuda_stream)
-    with torch.cuda.device(dev):
-        return fn(torch.cuda.current_stream(dev).cuda_stream)
+    """fn(stream) with `dev` current and torch's current HIP stream of it.
+
+    Reads the device and raw stream through torch's C bindings (the ones
+    Triton's launcher uses): torch.cuda.current_stream() resolves the device
+    through several Python layers and costs ~20 µs per call."""
+    cur = torch._C._cuda_getDevice()
+    idx = cur if dev.index is None else dev.index
+    if idx == cur:
+        return fn(torch._C._cuda_getCurrentRawStream(idx))
+    with torch.cuda.device(idx):
+        return fn(torch._C._cuda_getCurrentRawStream(idx))
 
 
 def _launch_fwd(lib, pr: SigattnProblem, out: torch.Tensor) -> None:
@@ -236,7 +242,7 @@ _CU_COUNT: dict = {}
 
 
 def _compute_units(device: torch.device) -> int:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+    idx = device.index if device.index is not None else torch._C._cuda_getDevice()
     n = _CU_COUNT.get(idx)
     if n is None:
         n = _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
@@ -378,10 +384,10 @@ def device_constant(shape, value, dtype: torch.dtype, device) -> torch.Tensor:
     Callers never write to it."""
     dev = torch.device(device)
     if (torch.compiler.is_compiling() or dev.type != "cuda"
-            or torch.cuda.is_current_stream_capturing()):
+            or torch._C._cuda_isCurrentStreamCapturing()):
         return torch.full(shape, value, dtype=dtype, device=dev)
     if dev.index is None:
-        dev = torch.device("cuda", torch.cuda.current_device())
+        dev = torch.device("cuda", torch._C._cuda_getDevice())
     key = (tuple(shape), float(value), dtype, dev)
     t = _CONSTANTS.get(key)
     if t is None:
