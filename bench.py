@@ -212,7 +212,9 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
 def cpu_baseline(cfg, budget_s: float = 20.0):
     """fp32 eager forward + autograd backward of the oracle's restatement of the
     reference's sigmoid_attention_ref, on the host cores, over a bounded slice
-    (first batch element, first few heads) of the same workload."""
+    of the same workload: as many heads of one batch element, then as many
+    batch elements (one at a time, so the L x L intermediates of only one are
+    live), as fit about `budget_s` over the three timed runs."""
     import torch
     from oracle.eager import fwd_bwd_fp32
     torch.set_num_threads(os.cpu_count() or 1)
@@ -220,25 +222,29 @@ def cpu_baseline(cfg, budget_s: float = 20.0):
     g = torch.Generator().manual_seed(0)
     heads = 1
     q, k, v, do = (torch.randn((1, L, heads, D), generator=g) for _ in range(4))
+    fwd_bwd_fp32(q, k, v, do, causal=causal)  # warm-up (thread pool, allocator)
     t0 = time.perf_counter()
-    fwd_bwd_fp32(q, k, v, do, causal=causal)  # warm-up
+    fwd_bwd_fp32(q, k, v, do, causal=causal)
     one = time.perf_counter() - t0
     heads = max(1, min(cfg["H"], int(budget_s / 3.0 / max(one, 1e-3))))
-    q, k, v, do = (torch.randn((1, L, heads, D), generator=g) for _ in range(4))
+    nb = max(1, min(cfg["B"], int(budget_s / 3.0 / max(one * heads, 1e-3))))
+    batches = [[torch.randn((1, L, heads, D), generator=g) for _ in range(4)] for _ in range(nb)]
     runs = []
     for _ in range(3):
         t0 = time.perf_counter()
-        fwd_bwd_fp32(q, k, v, do, causal=causal)
+        for q, k, v, do in batches:
+            fwd_bwd_fp32(q, k, v, do, causal=causal)
         runs.append(time.perf_counter() - t0)
     t = statistics.median(runs)
-    flops = 14 * D * pairs(L, causal) * heads
+    flops = 14 * D * pairs(L, causal) * heads * nb
     return {
         "value": round(flops / t / 1e12, 4),
         "unit": "TFLOPS",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"fp32 eager fwd+bwd (oracle/eager.py) on B=1 H={heads} of the same L={L} D={D} "
-                  f"causal={causal} workload, median of 3 after 1 warm-up, {t:.2f} s each",
+        "sample": f"fp32 eager fwd+bwd (oracle/eager.py) on B={nb} H={heads} (one batch element at a time) "
+                  f"of the same L={L} D={D} causal={causal} workload, median of 3 after warm-up, "
+                  f"{t:.2f} s each",
     }
 
 
