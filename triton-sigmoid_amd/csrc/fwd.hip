@@ -43,9 +43,11 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 ? 3 : 1)) void fwd_mfma_kernel(c
   constexpr int NKS = D / 16;           // MFMA k-steps over the head dim
   constexpr int NDB = D / 32;           // 32-row blocks of Oᵀ
   constexpr int NSTEP = NKS + 2 * NDB;  // steps (NCB MFMAs sharing an A operand) per region
-  // Operand read-ahead, in steps: 8 at D = 128 (2-7 % faster than 4 at the
-  // headline shapes), 4 at D = 64 (three waves per SIMD, 168 registers each).
-  constexpr int LA = D == 128 ? 8 : 4;
+  // Operand read-ahead, in steps.  D = 128: a whole region (16) without
+  // score_mod, 8 with it (16 would spill there); measured 2-3 % (8 vs 4) and
+  // another 1-2.5 % (16 vs 8) at the headline shapes.  D = 64: 4 (three waves
+  // per SIMD, 168 registers each).
+  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : 16) : 4;
   constexpr int NWD = 8 * NCB;          // packed P words per block
   constexpr int BAR = NSTEP - LA;       // step of the tile barrier in odd regions
   static_assert(NSTEP % LA == 0, "region shape");
