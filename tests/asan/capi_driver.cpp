@@ -1,0 +1,190 @@
+// Host-only driver for the address/undefined-behaviour sanitizer build of
+// csrc/capi.cpp (the C ABI's validation and dispatch).  The kernel launchers
+// are replaced by recorders, and hipGetLastError by a stub, so the program
+// needs no GPU and no HIP runtime initialisation: every call either returns
+// a validation error before any launch or records which launchers a valid
+// problem reaches.  Built and run by tests/test_capi_asan_cpu.py.
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "launch.h"
+#include "sigattn.h"
+
+namespace {
+std::vector<std::string> g_calls;
+sigattn::KParams g_last{};
+int g_fail = 0;
+
+void record(const char *name, const sigattn::KParams &p) {
+  g_calls.emplace_back(name);
+  g_last = p;
+}
+
+#define EXPECT(cond)                                                        \
+  do {                                                                      \
+    if (!(cond)) {                                                          \
+      std::fprintf(stderr, "%s:%d: expectation failed: %s\n", __FILE__, __LINE__, #cond); \
+      ++g_fail;                                                             \
+    }                                                                       \
+  } while (0)
+
+// Device pointers are never dereferenced on the host: any aligned address.
+void *const kFake = reinterpret_cast<void *>(uintptr_t(1) << 20);
+
+sigattn_problem base(int64_t B = 2, int64_t T = 16, int64_t H = 2, int64_t D = 64) {
+  sigattn_problem p;
+  std::memset(&p, 0, sizeof p);
+  p.abi_version = SIGATTN_ABI_VERSION;
+  p.dtype = SIGATTN_BF16;
+  p.B = B, p.Tq = T, p.Tk = T, p.H = H, p.D = D;
+  p.q_stride_b = p.k_stride_b = T * H * D;
+  p.q_stride_t = p.k_stride_t = H * D;
+  p.q_stride_h = p.k_stride_h = D;
+  p.q = p.k = p.v = kFake;
+  p.bias = p.scale = static_cast<const float *>(kFake);
+  return p;
+}
+
+std::string calls() {
+  std::string s;
+  for (auto &c : g_calls) s += (s.empty() ? "" : ",") + c;
+  g_calls.clear();
+  return s;
+}
+}  // namespace
+
+namespace sigattn {
+void launch_fwd_mfma(const KParams &p, int, int, bool, bool, hipStream_t) { record("fwd_mfma", p); }
+void launch_bwd_dq_mfma(const KParams &p, int, int, bool, bool, hipStream_t) { record("dq_mfma", p); }
+void launch_bwd_dkdv_mfma(const KParams &p, int, int, bool, bool, bool dsout, hipStream_t) {
+  record(dsout ? "dkdv_mfma_ds" : "dkdv_mfma", p);
+}
+void launch_bwd_dq_ds_mfma(const KParams &p, int, int, bool, hipStream_t) { record("dq_ds", p); }
+void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record("fwd_splitkv", p); }
+void launch_fwd_generic(const KParams &p, int, int, bool, hipStream_t) { record("fwd_generic", p); }
+void launch_bwd_dq_generic(const KParams &p, int, int, bool, hipStream_t) { record("dq_generic", p); }
+void launch_bwd_dkdv_generic(const KParams &p, int, int, bool, hipStream_t) { record("dkdv_generic", p); }
+}  // namespace sigattn
+
+// The library maps hipGetLastError() after its launches; no launch happens here.
+extern "C" hipError_t hipGetLastError(void) { return hipSuccess; }
+
+int main() {
+  // --- validation: the error codes of tests/test_capi_cpu.py, for every entry point
+  struct Bad {
+    const char *what;
+    void (*change)(sigattn_problem &);
+    int code;
+  } bad[] = {
+      {"abi", [](sigattn_problem &p) { p.abi_version = 99; }, SIGATTN_ERR_ABI_VERSION},
+      {"dtype", [](sigattn_problem &p) { p.dtype = 7; }, SIGATTN_ERR_DTYPE},
+      {"D48", [](sigattn_problem &p) { p.D = 48; }, SIGATTN_ERR_HEAD_DIM},
+      {"D256", [](sigattn_problem &p) { p.D = 256; }, SIGATTN_ERR_HEAD_DIM},
+      {"B<0", [](sigattn_problem &p) { p.B = -1; }, SIGATTN_ERR_SHAPE},
+      {"Tq huge", [](sigattn_problem &p) { p.Tq = int64_t(1) << 40; }, SIGATTN_ERR_SHAPE},
+      {"BH grid", [](sigattn_problem &p) { p.B = p.H = int64_t(1) << 30; }, SIGATTN_ERR_SHAPE},
+      {"stride", [](sigattn_problem &p) { p.k_stride_t = -5; }, SIGATTN_ERR_STRIDE},
+      {"dense Tq!=Tk", [](sigattn_problem &p) { p.Tk = 8; }, SIGATTN_ERR_DENSE_LENGTHS},
+      {"rows<0", [](sigattn_problem &p) { p.rows_q = -1, p.cu_seqlens_q = (const int32_t *)kFake; },
+       SIGATTN_ERR_SHAPE},
+      {"layout q", [](sigattn_problem &p) {
+         p.cu_seqlens_q = (const int32_t *)kFake, p.seq_lens_q = (const int32_t *)kFake; }, SIGATTN_ERR_LAYOUT},
+      {"layout k", [](sigattn_problem &p) {
+         p.cu_seqlens_k = (const int32_t *)kFake, p.seq_lens_k = (const int32_t *)kFake; }, SIGATTN_ERR_LAYOUT},
+      {"bias", [](sigattn_problem &p) { p.bias = nullptr; }, SIGATTN_ERR_NULL_ARG},
+      {"scale", [](sigattn_problem &p) { p.scale = nullptr; }, SIGATTN_ERR_NULL_ARG},
+      {"q", [](sigattn_problem &p) { p.q = nullptr; }, SIGATTN_ERR_NULL_ARG},
+      {"v", [](sigattn_problem &p) { p.v = nullptr; }, SIGATTN_ERR_NULL_ARG},
+  };
+  for (const Bad &b : bad) {
+    sigattn_problem p = base();
+    b.change(p);
+    EXPECT(sigattn_check(&p) == b.code);
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == b.code);
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, 1 << 20, nullptr) == b.code);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == b.code);
+    EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, kFake, 1 << 20, nullptr) == b.code);
+    EXPECT(sigattn_bwd_dq(&p, kFake, kFake, nullptr) == b.code);
+    EXPECT(sigattn_bwd_dkdv(&p, kFake, kFake, kFake, nullptr) == b.code);
+    EXPECT(sigattn_fwd_workspace_bytes(&p) == 0);
+    EXPECT(sigattn_bwd_workspace_bytes(&p) == 0);
+    if (!g_calls.empty()) std::fprintf(stderr, "case %s launched %s\n", b.what, calls().c_str());
+  }
+  EXPECT(sigattn_check(nullptr) == SIGATTN_ERR_NULL_ARG);
+  EXPECT(sigattn_fwd(nullptr, kFake, nullptr) == SIGATTN_ERR_NULL_ARG);
+  EXPECT(sigattn_bwd(nullptr, kFake, kFake, kFake, kFake, nullptr) == SIGATTN_ERR_NULL_ARG);
+  EXPECT(sigattn_fwd_workspace_bytes(nullptr) == 0 && sigattn_bwd_workspace_bytes(nullptr) == 0);
+  {
+    sigattn_problem p = base();
+    EXPECT(sigattn_fwd(&p, nullptr, nullptr) == SIGATTN_ERR_NULL_ARG);
+    EXPECT(sigattn_bwd(&p, kFake, nullptr, kFake, kFake, nullptr) == SIGATTN_ERR_NULL_ARG);
+    EXPECT(sigattn_bwd(&p, nullptr, kFake, kFake, kFake, nullptr) == SIGATTN_ERR_NULL_ARG);
+    EXPECT(sigattn_bwd_dkdv_ws(&p, kFake, kFake, kFake, nullptr, 1 << 20, nullptr) == SIGATTN_ERR_WORKSPACE);
+    EXPECT(sigattn_bwd_dq_ws(&p, kFake, nullptr, 1 << 20, nullptr) == SIGATTN_ERR_WORKSPACE);
+    EXPECT(g_calls.empty());
+  }
+  for (int code = -10; code <= 0; ++code) EXPECT(std::strlen(sigattn_strerror(code)) > 0);
+  EXPECT(std::strcmp(sigattn_strerror(-99), "unknown sigattn status") == 0);
+
+  // --- dispatch of valid problems
+  {
+    sigattn_problem p = base(2, 300, 3, 128);
+    p.causal = 1;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma");
+    EXPECT(g_last.B == 2 && g_last.H == 3 && g_last.Tq == 300 && g_last.out == kFake);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    const size_t ws = sigattn_bwd_workspace_bytes(&p);
+    EXPECT(ws == size_t(2) * 3 * (10 * 11 / 2) * 2048);
+    EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, kFake, ws, nullptr) == 0 &&
+           calls() == "dkdv_mfma_ds,dq_ds");
+    // Room for one head: three head groups, each dK/dV then dQ.
+    EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, kFake, ws / 3, nullptr) == 0 &&
+           calls() == "dkdv_mfma_ds,dq_ds,dkdv_mfma_ds,dq_ds,dkdv_mfma_ds,dq_ds");
+    EXPECT(g_last.H == 1 && g_last.ds_nqb == 10 && g_last.ds_nkb == 10);
+    // Less than one head: the recompute kernels.
+    EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, kFake, ws / 3 - 16, nullptr) == 0 &&
+           calls() == "dq_mfma,dkdv_mfma");
+    EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, (char *)kFake + 8, ws, nullptr) ==
+           SIGATTN_ERR_WORKSPACE);
+    EXPECT(sigattn_bwd_dkdv_ws(&p, kFake, kFake, kFake, kFake, ws - 1, nullptr) == SIGATTN_ERR_WORKSPACE);
+    EXPECT(g_calls.empty());
+  }
+  {
+    // fp32, D = 32, misaligned strides: the portable kernels.
+    sigattn_problem p = base(1, 40, 1, 32);
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");
+    p.D = 64;
+    p.dtype = SIGATTN_F32;
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_generic,dkdv_generic");
+    EXPECT(sigattn_bwd_workspace_bytes(&p) == 0);
+    p.dtype = SIGATTN_F16;
+    p.q_stride_t = 68;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");
+  }
+  {
+    // Decode shape: split-KV with a workspace, one chunk per (batch, head) without.
+    sigattn_problem p = base(1, 1, 1, 128);
+    p.Tk = 4096;
+    p.seq_lens_q = p.seq_lens_k = (const int32_t *)kFake;
+    p.k_stride_b = 4096 * 128;
+    const size_t ws = sigattn_fwd_workspace_bytes(&p);
+    EXPECT(ws == 16 * 128 * 4);
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, ws, nullptr) == 0 && calls() == "fwd_splitkv");
+    EXPECT(g_last.nsplit == 16 && g_last.chunk == 256 && g_last.ws == kFake);
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_splitkv");
+    EXPECT(g_last.nsplit == 1 && g_last.ws == nullptr);
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, ws - 1, nullptr) == SIGATTN_ERR_WORKSPACE && g_calls.empty());
+  }
+  {
+    // Empty problems launch nothing.
+    sigattn_problem p = base(0, 16, 2, 64);
+    EXPECT(sigattn_fwd(&p, nullptr, nullptr) == 0 && sigattn_bwd(&p, nullptr, nullptr, nullptr, nullptr, nullptr) == 0);
+    p = base(2, 0, 2, 64);
+    EXPECT(sigattn_fwd(&p, nullptr, nullptr) == 0 && sigattn_bwd(&p, nullptr, nullptr, nullptr, nullptr, nullptr) == 0);
+    EXPECT(g_calls.empty());
+  }
+  if (g_fail == 0) std::printf("capi sanitizer driver: all checks passed\n");
+  return g_fail == 0 ? 0 : 1;
+}

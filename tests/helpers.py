@@ -46,3 +46,57 @@ def assert_close_to_oracle(got: torch.Tensor, want: np.ndarray, dtype, name: str
     err = float(np.abs(g - want).max()) if want.size else 0.0
     assert err <= bound, f"{name}: max abs err {err:.3e} > bound {bound:.3e} (max|ref| {scale:.3e})"
     return err
+
+
+def _threads() -> int:
+    import os
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def criterion_errors(q, k, v, do, ours_fn, eager_kw, q_valid=None, k_valid=None):
+    """The reference tests' error pair (tests/test_sigmoid_dense.py:77-166,
+    tests/test_sigmoid_padded.py:76-186): max-abs error of our kernel and of
+    the mixed-precision eager path (upcast=False, reorder_ops=True), both
+    against the fp32 eager path (upcast=True), for O, dQ, dK, dV.
+
+    The fp32 path runs on the GPU.  The mixed-precision path runs on the CPU:
+    its bf16 / fp16 batched products and their backward transpose operands
+    inside torch, which this pool's GPUs must not be given.
+    q_valid [B, Tq] / k_valid [B, Tk] (bool) restrict errors to valid rows.
+    Returns {name: (err_ours, err_mixed)}."""
+    from oracle.eager import sigmoid_attention_eager
+    dev = q.device
+    qm = None if q_valid is None else q_valid.to(dev)[:, :, None, None]
+    km = None if k_valid is None else k_valid.to(dev)[:, :, None, None]
+
+    def run(fn, tensors):
+        leaves = [t.detach().clone().requires_grad_(True) for t in tensors[:3]]
+        o = fn(*leaves)
+        o.backward(tensors[3].to(o.dtype))
+        return [o.detach()] + [t.grad for t in leaves]
+
+    ours = run(ours_fn, (q, k, v, do))
+    ref = run(lambda a, b, c: sigmoid_attention_eager(a, b, c, upcast=True, **eager_kw), (q, k, v, do))
+    torch.set_num_threads(_threads())
+    cpu_kw = {n: (x.cpu() if torch.is_tensor(x) else x) for n, x in eager_kw.items()}
+    mixed = run(lambda a, b, c: sigmoid_attention_eager(a, b, c, upcast=False, reorder_ops=True, **cpu_kw),
+                tuple(t.cpu() for t in (q, k, v, do)))
+    out = {}
+    for i, name in enumerate(("O", "dQ", "dK", "dV")):
+        mask = qm if name in ("O", "dQ") else km
+        r = ref[i].float()
+        e = (ours[i].float() - r)
+        em = (mixed[i].to(dev).float() - r)
+        if mask is not None:
+            e, em = e * mask, em * mask
+        out[name] = (e.abs().max().item(), em.abs().max().item())
+    return out
+
+
+def assert_reference_criterion(errs, tol):
+    """fwd: err <= 2 err_mixed + tol and err < tol; bwd: 3x (the reference's
+    tests/test_sigmoid_dense.py:111-114,154-166)."""
+    for name, (e, em) in errs.items():
+        f = 2.0 if name == "O" else 3.0
+        assert e <= f * em + tol, (name, e, em, tol)
+        assert e < tol, (name, e, tol)

@@ -242,3 +242,46 @@ def test_device_code_has_no_packed_fp32_instructions(src):
     asm = subprocess.run(cmd, capture_output=True, text=True, check=True).stdout
     assert "v_mfma" in asm or src == "generic.hip"
     assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)
+
+
+def test_backward_workspace_oom_falls_back_to_recompute(monkeypatch):
+    """An out-of-memory error while allocating the two-pass dS workspace
+    gives no workspace (the recompute backward runs) instead of failing."""
+    def no_memory(*a, **k):
+        raise torch.OutOfMemoryError("forced: no device memory for the workspace")
+    assert _capi._bwd_workspace(0, torch.device("cpu")) == (None, 0)
+    ws, n = _capi._bwd_workspace(64, torch.device("cpu"))
+    assert n == 64 and ws.numel() == 64
+    monkeypatch.setattr(_capi.torch, "empty", no_memory)
+    assert _capi._bwd_workspace(1 << 30, torch.device("cpu")) == (None, 0)
+
+
+def test_device_constants_are_never_freed(monkeypatch):
+    """Cached constants stay alive for the process (a kernel queued on any
+    stream may still read one); past the cap, calls get uncached tensors."""
+    made = []
+    monkeypatch.setattr(_capi, "_CONSTANTS", {})
+    monkeypatch.setattr(_capi, "_CONSTANTS_MAX", 3)
+    monkeypatch.setattr(torch._C, "_cuda_isCurrentStreamCapturing", lambda: False)
+    monkeypatch.setattr(torch._C, "_cuda_getDevice", lambda: 0)
+
+    class _T:
+        def __init__(self, v):
+            self.v = v
+
+        def to(self, dev):
+            made.append(self)
+            return self
+
+    real_full = torch.full
+    monkeypatch.setattr(_capi.torch, "full",
+                        lambda shape, value, dtype=None, device=None: _T(value) if device is None
+                        else real_full(shape, value, dtype=dtype))
+    first = [_capi.device_constant((2,), float(i), torch.float32, "cuda:0") for i in range(3)]
+    assert len(made) == 3 and len(_capi._CONSTANTS) == 3
+    again = [_capi.device_constant((2,), float(i), torch.float32, "cuda:0") for i in range(3)]
+    assert all(a is b for a, b in zip(first, again))
+    extra = _capi.device_constant((2,), 9.0, torch.float32, "cuda:0")
+    assert isinstance(extra, torch.Tensor) and len(_capi._CONSTANTS) == 3
+    assert all(_capi._CONSTANTS[((2,), float(i), torch.float32, torch.device("cuda", 0))] is first[i]
+               for i in range(3))

@@ -9,7 +9,8 @@ import torch
 
 import triton_sigmoid as ts
 from conftest import get_tolerance
-from helpers import assert_close_to_oracle, oracle_fwd_bwd, randn
+from helpers import (assert_close_to_oracle, assert_reference_criterion, criterion_errors,
+                     oracle_fwd_bwd, randn)
 from oracle.eager import sigmoid_attention_eager
 
 pytestmark = pytest.mark.gpu
@@ -87,37 +88,21 @@ def test_dense_score_mod_matches_oracle(dtype, D, causal):
 
 
 # --- the reference's own criterion (tests/test_sigmoid_dense.py:35-166) -------
+# Same grid as the reference's test_dense_op: B, H in {(1, 2), (4, 8)},
+# T in {128 ... 4096}, D in {64, 128}, causal, fp16 / bf16 / fp32.
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,H", [(1, 2), (4, 8)])
-@pytest.mark.parametrize("T", [128, 1024, 4096])
+@pytest.mark.parametrize("T", [128, 256, 512, 1024, 2048, 4096])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_dense_reference_criterion(dtype, B, H, T, D, causal):
-    if dtype == torch.float32 and T == 4096 and B == 4:
-        pytest.skip("fp32 takes the portable kernel; the large fp32 case only adds run time")
     tol = get_tolerance(dtype)
     q, k, v, do = _inputs(B, T, H, D, dtype, seed=B + T + D, std=0.5)
-    do = do.float() * 2.0  # N(0, 1) like torch.randn_like(out) in the reference test
-    leaves = {}
-    outs = {}
-    for name in ("ref", "pt", "ours"):
-        leaves[name] = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
-    outs["ref"] = sigmoid_attention_eager(*leaves["ref"], upcast=True, causal=causal)
-    outs["pt"] = sigmoid_attention_eager(*leaves["pt"], upcast=False, reorder_ops=True, causal=causal)
-    outs["ours"] = ts.sigmoid_attention(*leaves["ours"], is_causal=causal)
-    err = (outs["ours"].float() - outs["ref"].float()).abs().max().item()
-    err_pt = (outs["pt"].float() - outs["ref"].float()).abs().max().item()
-    assert err <= 2 * err_pt + tol, (err, err_pt)
-    assert err < tol, err
-    for name in outs:
-        outs[name].backward(do.to(outs[name].dtype))
-    for i, gname in enumerate("qkv"):
-        ref_g = leaves["ref"][i].grad.float()
-        e = (leaves["ours"][i].grad.float() - ref_g).abs().max().item()
-        e_pt = (leaves["pt"][i].grad.float() - ref_g).abs().max().item()
-        assert e <= 3 * e_pt + tol, (gname, e, e_pt)
-        assert e < tol, (gname, e)
+    do = (do.float() * 2.0).to(dtype)  # N(0, 1) like torch.randn_like(out) in the reference test
+    errs = criterion_errors(q, k, v, do, lambda a, b, c: ts.sigmoid_attention(a, b, c, is_causal=causal),
+                            dict(causal=causal))
+    assert_reference_criterion(errs, tol)
 
 
 # --- BASELINE parity bar: max-abs <= 2e-2 vs fp32 eager at N(0,1) --------------
@@ -153,6 +138,26 @@ def test_baseline_configs_within_2e2(cfg):
     for name, got, want in (("O", o, ro), ("dQ", q.grad, rq), ("dK", k.grad, rk), ("dV", v.grad, rv)):
         err = (got.float() - want).abs().max().item()
         assert err <= 2e-2, (name, err)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_c1_fp32_matches_oracle(causal):
+    """fp32 B=2 L=256 H=4 D=64, q/k/v/dO ~ N(0,1)
+    from a seed, scale 1/sqrt(D), default bias -log(L), fwd+bwd through the
+    public API (the portable fp32 kernels) against the float64 oracle."""
+    B, T, H, D = 2, 256, 4, 64
+    q, k, v, do = _inputs(B, T, H, D, torch.float32, seed=0)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=causal)
+    o.backward(do)
+    bias = np.full(B, -math.log(T), dtype=np.float32).astype(np.float64)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1.0 / math.sqrt(D)), bias=bias,
+                                          causal=causal)
+    assert_close_to_oracle(o, want_o, torch.float32, "O")
+    assert_close_to_oracle(q.grad, dq, torch.float32, "dQ")
+    assert_close_to_oracle(k.grad, dk, torch.float32, "dK")
+    assert_close_to_oracle(v.grad, dv, torch.float32, "dV")
 
 
 # --- behaviour -----------------------------------------------------------------

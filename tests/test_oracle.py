@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import sigmoid_oracle as so
-from oracle.eager import sigmoid_attention_eager
+from oracle.eager import fwd_bwd_fp32, sigmoid_attention_eager
 
 
 def _rand(rng, *shape):
@@ -278,3 +278,84 @@ def test_negative_and_oversized_seq_lens_are_clamped():
     assert np.all(o[0] == 0)           # no valid queries
     assert np.all(o[1] == 0)           # no valid keys
     assert np.all(np.isfinite(o))
+
+
+# ------------------------------------------- fp32 eager checker (upcast) --
+# oracle/eager.py's upcast=True branch and fwd_bwd_fp32 decide the full-size
+# GPU tests (BASELINE configs c2-c5 within 2e-2) and the "ref" side of every
+# reference-criterion test, so they are pinned here against the float64
+# oracle, which the closed forms, loops, finite differences and autograd
+# above pin in turn.  A dropped bias, a scale on the wrong operand, a
+# triu offset off by one or a key mask applied before the sigmoid each move
+# the fp32 result by far more than fp32 rounding.
+
+def _fp32_case(rng, B, Tq, Tk, H, D):
+    return [torch.tensor(_rand(rng, B, t, H, D), dtype=torch.float32) for t in (Tq, Tk, Tk, Tq)]
+
+
+def _fp32_bound(want, n_terms):
+    # fp32 accumulation of n_terms products: relative error well under
+    # n_terms * 2^-24 of the largest magnitude.
+    return 8.0 * n_terms * 2.0 ** -24 * float(np.abs(want).max()) + 1e-7
+
+
+@pytest.mark.parametrize("case", ["dense", "causal", "padded_cross", "padded_causal", "score_mod", "explicit_bias"])
+def test_eager_fp32_matches_oracle(case):
+    rng = np.random.default_rng(40 + len(case))
+    B, H, D = 2, 3, 16
+    Tq, Tk = (9, 13) if case == "padded_cross" else (11, 11)
+    q, k, v, do = _fp32_case(rng, B, Tq, Tk, H, D)
+    kw = dict(causal=case in ("causal", "padded_causal", "score_mod"))
+    sq = sk = sm = None
+    if case.startswith("padded"):
+        sq = torch.tensor([Tq - 3, Tq], dtype=torch.int32)
+        sk = torch.tensor([Tk, Tk - 5], dtype=torch.int32)
+        kw.update(seq_lens_q=sq, seq_lens_k=sk)
+    if case == "score_mod":
+        sm = torch.tensor(_rand(rng, B, Tk), dtype=torch.float32)
+        kw["score_mod"] = sm
+    scale = 0.37 if case == "explicit_bias" else None
+    if case == "explicit_bias":
+        kw.update(scale=scale, sigmoid_bias=-1.25)
+    # The bias the eager path uses: explicit, else -log(len + 1e-6) in fp32
+    # (padded) or in float64 (dense), as sigmoid_reference.py:73-80 does.
+    if case == "explicit_bias":
+        bias = np.full(B, -1.25)
+    elif sk is not None:
+        bias = (-torch.log(sk.float() + 1e-6)).double().numpy()
+    else:
+        bias = np.full(B, -math.log(Tk + 1e-6))
+    okw = dict(scale=np.float32(scale if scale is not None else 1.0 / math.sqrt(D)), bias=bias,
+               score_mod=None if sm is None else sm.double().numpy(),
+               seq_lens_q=None if sq is None else sq.numpy(), seq_lens_k=None if sk is None else sk.numpy(),
+               causal=kw["causal"])
+    qn, kn, vn, dn = (t.double().numpy() for t in (q, k, v, do))
+    want_o = so.forward(qn, kn, vn, **okw)
+    want_g = so.backward(qn, kn, vn, dn, **okw)
+
+    o = sigmoid_attention_eager(q, k, v, upcast=True, **kw)
+    assert o.dtype == torch.float32
+    np.testing.assert_allclose(o.double().numpy(), want_o, rtol=0, atol=_fp32_bound(want_o, D + Tk))
+    o2, dq, dk, dv = fwd_bwd_fp32(q, k, v, do, **kw)
+    np.testing.assert_array_equal(o2.numpy(), o.numpy())
+    for name, got, want in zip(("dQ", "dK", "dV"), (dq, dk, dv), want_g):
+        np.testing.assert_allclose(got.double().numpy(), want, rtol=0,
+                                   atol=_fp32_bound(want, D + Tq + Tk), err_msg=name)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_eager_fp32_at_c1_matches_oracle(causal):
+    """BASELINE.json configs[0] (CPU plumbing): fp32 B=2 L=256 H=4 D=64,
+    q/k/v/dO ~ N(0,1) from a seed, scale 1/sqrt(D), default bias, fwd+bwd."""
+    B, L, H, D = 2, 256, 4, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn((B, L, H, D), generator=g) for _ in range(4))
+    o, dq, dk, dv = fwd_bwd_fp32(q, k, v, do, causal=causal)
+    okw = dict(scale=np.float32(1.0 / math.sqrt(D)), bias=np.full(B, -math.log(L + 1e-6)), causal=causal)
+    qn, kn, vn, dn = (t.double().numpy() for t in (q, k, v, do))
+    want_o = so.forward(qn, kn, vn, **okw)
+    want_g = so.backward(qn, kn, vn, dn, **okw)
+    for name, got, want in zip(("O", "dQ", "dK", "dV"), (o, dq, dk, dv), (want_o, *want_g)):
+        err = float(np.abs(got.double().numpy() - want).max())
+        # fp32 sums of a few hundred terms: ~1e-6 of the largest magnitude.
+        assert err <= 4e-6 * float(np.abs(want).max()) + 1e-6, (name, err)

@@ -10,8 +10,8 @@ import torch
 
 import triton_sigmoid as ts
 from conftest import get_tolerance
-from helpers import assert_close_to_oracle, oracle_fwd_bwd, randn, to_np
-from oracle.eager import sigmoid_attention_eager
+from helpers import (assert_close_to_oracle, assert_reference_criterion, criterion_errors,
+                     oracle_fwd_bwd, randn, to_np)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -143,30 +143,27 @@ def test_padded_many_batches_odd_key_blocks(causal):
         assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+# The reference's test_op grid (tests/test_sigmoid_padded.py:48-186): B, H in
+# {(1, 2), (4, 8)}, (Tq, Tk) pairs, D in {64, 128}, causal (skipped for
+# Tq > Tk, as there), fp16 / bf16 / fp32, seq_lens ~ U[0.8 T, T], N(0, 0.5²)
+# inputs; errors on valid rows only.
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,H", [(1, 2), (4, 8)])
+@pytest.mark.parametrize("Tq,Tk", [(128, 128), (256, 512), (512, 256), (1024, 1024), (4096, 4096)])
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_padded_reference_criterion(dtype, causal):
-    """tests/test_sigmoid_padded.py:48-186 criterion with seq_lens ~ U[0.8T, T]."""
-    B, T, H, D = 4, 1024, 4, 128
+def test_padded_reference_criterion(dtype, B, H, Tq, Tk, D, causal):
+    if causal and Tq > Tk:
+        pytest.skip("causal needs Tq <= Tk (the reference skips it too)")
     tol = get_tolerance(dtype)
-    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=21, std=0.5, noise=False, lo=0.8)
-    leaves = {n: [t.detach().clone().requires_grad_(True) for t in (q, k, v)] for n in ("ref", "pt", "ours")}
-    outs = {
-        "ref": sigmoid_attention_eager(*leaves["ref"], seq_lens_k=sk, seq_lens_q=sq, upcast=True, causal=causal),
-        "pt": sigmoid_attention_eager(*leaves["pt"], seq_lens_k=sk, seq_lens_q=sq, upcast=False,
-                                      reorder_ops=True, causal=causal),
-        "ours": ts.sigmoid_attention_padded(*leaves["ours"], seq_lens_k=sk, seq_lens_q=sq, is_causal=causal),
-    }
-    err = (outs["ours"].float() - outs["ref"].float()).abs().max().item()
-    err_pt = (outs["pt"].float() - outs["ref"].float()).abs().max().item()
-    assert err <= 2 * err_pt + tol and err < tol, (err, err_pt)
-    for n in outs:
-        outs[n].backward(do)
-    for i, gname in enumerate("qkv"):
-        ref_g = leaves["ref"][i].grad.float()
-        e = (leaves["ours"][i].grad.float() - ref_g).abs().max().item()
-        e_pt = (leaves["pt"][i].grad.float() - ref_g).abs().max().item()
-        assert e <= 3 * e_pt + tol and e < tol, (gname, e, e_pt)
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=Tq + 3 * Tk + D + B, std=0.5, noise=False, lo=0.8)
+    q_valid = torch.arange(Tq)[None, :] < sq.cpu()[:, None]
+    k_valid = torch.arange(Tk)[None, :] < sk.cpu()[:, None]
+    errs = criterion_errors(
+        q, k, v, do,
+        lambda a, b, c: ts.sigmoid_attention_padded(a, b, c, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal),
+        dict(seq_lens_k=sk, seq_lens_q=sq, causal=causal), q_valid=q_valid, k_valid=k_valid)
+    assert_reference_criterion(errs, tol)
 
 
 def test_padding_noise_invariance():

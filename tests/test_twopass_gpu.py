@@ -284,3 +284,35 @@ def test_public_api_uses_two_pass_at_d128(causal, monkeypatch):
     _assert_twopass_matches(grads[1], grads[0], dtype)
     for a, b in zip(grads[2], grads[1]):
         assert torch.equal(a, b)
+
+
+def test_workspace_allocation_failure_falls_back_to_recompute(monkeypatch):
+    """When the dS workspace cannot be allocated the backward still runs (the
+    recompute kernels) and gives exactly the recompute backward's gradients."""
+    import triton_sigmoid as ts
+    B, T, H, D = 2, 384, 4, 128
+    dtype = torch.bfloat16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=22)
+    grads = []
+    real_empty = torch.empty
+    calls = []
+
+    def failing_empty(*a, dtype=None, **kw):
+        if dtype == torch.uint8:
+            calls.append(a)
+            raise torch.OutOfMemoryError("forced: no device memory for the dS workspace")
+        return real_empty(*a, dtype=dtype, **kw)
+
+    for mode in ("recompute", "oom"):
+        if mode == "recompute":
+            monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "0")
+        else:
+            monkeypatch.delenv("SIGATTN_BWD_WORKSPACE_MB", raising=False)
+            monkeypatch.setattr(_capi.torch, "empty", failing_empty)
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        ts.sigmoid_attention(*leaves, is_causal=True).backward(do)
+        grads.append([t.grad for t in leaves])
+        monkeypatch.setattr(_capi.torch, "empty", real_empty)
+    assert calls, "the two-pass workspace allocation was not attempted"
+    for a, b in zip(grads[0], grads[1]):
+        assert torch.equal(a, b)

@@ -273,12 +273,25 @@ def bwd_workspace_bytes(lib, pr: SigattnProblem, device: torch.device) -> int:
     return heads * per_head
 
 
+def _bwd_workspace(nbytes: int, device: torch.device):
+    """The two-pass backward's dS workspace, or None when it is not used or
+    the device cannot hold it: the recompute backward needs no workspace, so
+    an allocation failure falls back to it instead of failing the backward
+    (the reference's backward allocates only its outputs)."""
+    if nbytes == 0:
+        return None, 0
+    try:
+        return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+    except torch.OutOfMemoryError:
+        return None, 0
+
+
 def _launch_bwd(lib, pr: SigattnProblem, dO, dQ, dK, dV) -> None:
     """sigattn_bwd_ws with a workspace from torch's caching allocator when
-    the two-pass backward applies (bwd_workspace_bytes), else sigattn_bwd."""
+    the two-pass backward applies (bwd_workspace_bytes) and the allocation
+    succeeds, else sigattn_bwd (the recompute kernels)."""
     def run(stream):
-        nbytes = bwd_workspace_bytes(lib, pr, dQ.device)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dQ.device) if nbytes else None
+        ws, nbytes = _bwd_workspace(bwd_workspace_bytes(lib, pr, dQ.device), dQ.device)
         _raise(lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
                                   stream), "sigattn_bwd_ws")
 
@@ -378,8 +391,8 @@ def device_constant(shape, value, dtype: torch.dtype, device) -> torch.Tensor:
     """A device tensor of `shape` filled with `value`, for the per-call bias /
     scale / default-length tensors of the public APIs.  Eagerly the tensor is
     made once per (shape, value, dtype, device) by a blocking host-to-device
-    copy (complete before first use on any stream) and reused, so a call
-    launches no fill kernels; under torch.compile it is an ordinary
+    copy (complete before first use on any stream), kept for the life of the
+    process and reused, so a call launches no fill kernels; under torch.compile it is an ordinary
     torch.full in the graph, and under CUDA-graph capture a captured fill.
     Callers never write to it."""
     dev = torch.device(device)
@@ -392,7 +405,11 @@ def device_constant(shape, value, dtype: torch.dtype, device) -> torch.Tensor:
     t = _CONSTANTS.get(key)
     if t is None:
         if len(_CONSTANTS) >= _CONSTANTS_MAX:
-            _CONSTANTS.clear()
+            # Cached tensors are never freed: a kernel still queued on any
+            # stream may read one.  Past the cap, a per-call tensor filled on
+            # the current stream (freed by torch's allocator in that stream's
+            # order) takes its place.
+            return torch.full(shape, value, dtype=dtype, device=dev)
         t = torch.full(shape, value, dtype=dtype).to(dev)
         _CONSTANTS[key] = t
     return t
