@@ -48,10 +48,6 @@ def assert_close_to_oracle(got: torch.Tensor, want: np.ndarray, dtype, name: str
     return err
 
 
-def _threads() -> int:
-    import os
-    return max(1, min(16, os.cpu_count() or 1))
-
 
 def criterion_errors(q, k, v, do, ours_fn, eager_kw, q_valid=None, k_valid=None):
     """The reference tests' error pair (tests/test_sigmoid_dense.py:77-166,
@@ -59,12 +55,14 @@ def criterion_errors(q, k, v, do, ours_fn, eager_kw, q_valid=None, k_valid=None)
     the mixed-precision eager path (upcast=False, reorder_ops=True), both
     against the fp32 eager path (upcast=True), for O, dQ, dK, dV.
 
-    The fp32 path runs on the GPU.  The mixed-precision path runs on the CPU:
-    its bf16 / fp16 batched products and their backward transpose operands
-    inside torch, which this pool's GPUs must not be given.
+    Both run on the inputs' device.  The fp32 path goes through autograd in
+    fp32; the mixed-precision path is oracle/eager.py's mixed_fwd_bwd, whose
+    bf16 / fp16 products all take contiguous operands (autograd through the
+    eager einsums would hand torch's batched products transposed views, which
+    this pool's GPUs must not be given in bf16).
     q_valid [B, Tq] / k_valid [B, Tk] (bool) restrict errors to valid rows.
     Returns {name: (err_ours, err_mixed)}."""
-    from oracle.eager import sigmoid_attention_eager
+    from oracle.eager import mixed_fwd_bwd, sigmoid_attention_eager
     dev = q.device
     qm = None if q_valid is None else q_valid.to(dev)[:, :, None, None]
     km = None if k_valid is None else k_valid.to(dev)[:, :, None, None]
@@ -77,10 +75,7 @@ def criterion_errors(q, k, v, do, ours_fn, eager_kw, q_valid=None, k_valid=None)
 
     ours = run(ours_fn, (q, k, v, do))
     ref = run(lambda a, b, c: sigmoid_attention_eager(a, b, c, upcast=True, **eager_kw), (q, k, v, do))
-    torch.set_num_threads(_threads())
-    cpu_kw = {n: (x.cpu() if torch.is_tensor(x) else x) for n, x in eager_kw.items()}
-    mixed = run(lambda a, b, c: sigmoid_attention_eager(a, b, c, upcast=False, reorder_ops=True, **cpu_kw),
-                tuple(t.cpu() for t in (q, k, v, do)))
+    mixed = mixed_fwd_bwd(q, k, v, do, **eager_kw)
     out = {}
     for i, name in enumerate(("O", "dQ", "dK", "dV")):
         mask = qm if name in ("O", "dQ") else km

@@ -359,3 +359,50 @@ def test_eager_fp32_at_c1_matches_oracle(causal):
         err = float(np.abs(got.double().numpy() - want).max())
         # fp32 sums of a few hundred terms: ~1e-6 of the largest magnitude.
         assert err <= 4e-6 * float(np.abs(want).max()) + 1e-6, (name, err)
+
+
+# -------------------------- mixed-precision eager path, written out (GPU use) --
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.float64])
+@pytest.mark.parametrize("case", ["dense", "causal", "padded", "score_mod", "padded_causal_sm"])
+def test_mixed_fwd_bwd_matches_autograd(dtype, case):
+    """oracle/eager.py's mixed_fwd_bwd (contiguous matmuls, backward by hand)
+    against autograd through sigmoid_attention_eager(upcast=False,
+    reorder_ops=True), the reference's mixed-precision path: same values up
+    to the summation order of the products (bit for bit on this CPU)."""
+    from oracle.eager import mixed_fwd_bwd
+    g = torch.Generator().manual_seed(hash(case) % 1000)
+    B, Lq, H, D = 2, 40, 3, 32
+    Lk = 56 if case == "padded" else 40
+    q, k, v = ((torch.randn(B, t, H, D, generator=g) * 0.5).to(dtype) for t in (Lq, Lk, Lk))
+    do = torch.randn(B, Lq, H, D, generator=g).to(dtype)
+    kw = dict(causal=case in ("causal", "padded_causal_sm"))
+    if case.startswith("padded"):
+        kw.update(seq_lens_q=torch.tensor([Lq - 5, Lq], dtype=torch.int32),
+                  seq_lens_k=torch.tensor([Lk, Lk - 9], dtype=torch.int32))
+    if case in ("score_mod", "padded_causal_sm"):
+        kw["score_mod"] = torch.randn(B, Lk, generator=g).to(dtype)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = sigmoid_attention_eager(*leaves, upcast=False, reorder_ops=True, **kw)
+    o.backward(do)
+    want = [o.detach()] + [t.grad for t in leaves]
+    got = mixed_fwd_bwd(q, k, v, do, **kw)
+    ulp = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24,
+           torch.float64: 2.0 ** -53}[dtype]
+    for name, a, b in zip(("O", "dQ", "dK", "dV"), got, want):
+        assert a.dtype == b.dtype and a.shape == b.shape, name
+        err = (a.double() - b.double()).abs().max().item()
+        assert err <= ulp * b.double().abs().max().item(), (name, err)
+    if dtype == torch.float64:
+        # In float64 the path is exact math: the float64 oracle, with the
+        # eager bias -log(L + 1e-6) (padded: computed in fp32, as there).
+        sq, sk = kw.get("seq_lens_q"), kw.get("seq_lens_k")
+        bias = ((-torch.log(sk.float() + 1e-6)).double().numpy() if sk is not None
+                else np.full(B, -math.log(Lk + 1e-6)))
+        okw = dict(scale=1.0 / math.sqrt(D), bias=bias, causal=kw["causal"],
+                   score_mod=None if "score_mod" not in kw else kw["score_mod"].numpy(),
+                   seq_lens_q=None if sq is None else sq.numpy(), seq_lens_k=None if sk is None else sk.numpy())
+        arrs = [t.numpy() for t in (q, k, v, do)]
+        for name, a, b in zip(("O", "dQ", "dK", "dV"), got,
+                              (so.forward(*arrs[:3], **okw), *so.backward(*arrs, **okw))):
+            np.testing.assert_allclose(a.numpy(), b, rtol=1e-12, atol=1e-13, err_msg=name)

@@ -164,8 +164,9 @@ def sigmoid_attention_varlen(
             dtype, converted to int32) with cu[0] = 0 and cu[B] = total rows;
             sequence b is rows cu[b] .. cu[b+1]-1.
         max_seqlen_q / max_seqlen_k: the longest query / key sequence (at
-            least every length).  None reads it from cu_seqlens (one device
-            to host copy).
+            least every length: a sequence longer than it is cut to its
+            first max_seqlen rows, as flash_attn_varlen_func's contract has
+            it).  None reads it from cu_seqlens (one device to host copy).
         is_causal: query i of a sequence attends to its keys j <= i.
         scale: default 1/sqrt(D).
         sigmoid_bias: default -log(key length of each sequence).
@@ -174,9 +175,13 @@ def sigmoid_attention_varlen(
 
     Returns:
         [total_q, H, D] output, equal row for row to what
-        `sigmoid_attention_padded` returns for the same sequences.  Rows
-        outside every sequence (when cu does not cover all rows) are not
-        written.
+        `sigmoid_attention_padded` returns for the same sequences.
+
+    Rows outside every sequence are never written, in the output or in the
+    gradients: rows past cu[B] when cu does not cover all rows, and rows past
+    max_seqlen of a longer sequence, hold whatever the freshly allocated
+    tensors held (uninitialised memory).  Callers that pass such rows must
+    ignore those rows of dQ / dK / dV, or make cu_seqlens cover every row.
     """
     if query.dim() != 3 or key.dim() != 3 or value.dim() != 3:
         raise ValueError("Expected query, key, and value to be 3D tensors (total_tokens, H, D)")
