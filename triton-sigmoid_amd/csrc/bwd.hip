@@ -50,8 +50,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     b = it.b, h = it.h, qb = it.blk;
   } else {
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    qb = blockIdx.x / BH;
+    int bh;
+    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb);
     if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }
@@ -258,8 +258,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     b = it.b, h = it.h, kblk = it.blk;
   } else {
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    kblk = blockIdx.x / BH;  // causal: low key blocks carry the most work and come first
+    int bh;
+    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, kblk);  // causal: low key blocks (the most work) first
     b = bh / p.H, h = bh % p.H;
   }
   const int Lq = p.len_q(b);
@@ -615,8 +615,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
     b = it.b, h = it.h, kblk0 = it.blk, nitems = 1;
   } else {
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    kblk0 = blockIdx.x / BH;
+    int bh;
+    dense_item(blockIdx.x, BH, (int)(gridDim.x / BH), !CAUSAL, bh, kblk0);
     nitems = p.nblk - 1 - kblk0 > kblk0 ? 2 : 1;
     b = bh / p.H, h = bh % p.H;
   }
@@ -988,8 +988,8 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) 
     b = it.b, h = it.h, qblk = it.blk;
   } else {
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    qblk = blockIdx.x / BH;
+    int bh;
+    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qblk);
     if (CAUSAL) qblk = p.nblk - 1 - qblk;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }

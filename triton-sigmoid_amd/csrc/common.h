@@ -213,6 +213,31 @@ struct WorkOrder {
   }
 };
 
+// Dense grids (every (batch, head) pair has the same `nper` row blocks): the
+// pair and row block of workgroup `id`.  The hardware deals workgroup ids
+// round-robin over the 8 XCDs, each with its own L2, and each XCD starts its
+// ids in order.
+//   * Equal items (grouped): XCD x gets the consecutive pairs x*BH/8 .. , all
+//     row blocks of one pair back to back, so the rows those blocks share (K
+//     and V, or Q and dO) are read while they sit in one L2; with `id % BH`
+//     as the pair, every XCD would cycle through BH/8 pairs at once.
+//   * Unequal items (causal, !grouped): `id % BH`, `id / BH`, so that every
+//     XCD starts the row-block levels in the order the caller maps them to
+//     (heaviest first); grouping pairs there broke that order and made the
+//     causal kernels slower (measured at B=4 L=4096 H=16 D=128: dQ from dS
+//     0.254 -> 0.322 ms, forward 0.30 -> 0.33 ms).
+// B*H not a multiple of 8 keeps the plain order.
+__device__ __forceinline__ void dense_item(int id, int BH, int nper, bool grouped, int &bh, int &blk) {
+  if (!grouped || BH % 8 != 0) {
+    bh = id % BH;
+    blk = id / BH;
+    return;
+  }
+  const int j = id >> 3;
+  bh = (id & 7) * (BH >> 3) + j / nper;
+  blk = j % nper;
+}
+
 // ---------------------------------------------------------------------------
 // dS workspace of the two-pass backward.  dS of (batch, head) is cut into
 // 32-query x 32-key tiles of 2 KB, stored column by column (key block kb,

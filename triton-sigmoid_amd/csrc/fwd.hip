@@ -65,8 +65,8 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 ? 3 : 1)) void fwd_mfma_kernel(c
     b = it.b, h = it.h, qb = it.blk;
   } else {
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    qb = blockIdx.x / BH;
+    int bh;
+    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb);
     if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }
