@@ -50,7 +50,9 @@ enum sigattn_status {
   SIGATTN_ERR_ABI_VERSION = -7,   /* problem.abi_version != SIGATTN_ABI_VERSION */
   SIGATTN_ERR_LAUNCH = -8,        /* hipGetLastError() reported a failure */
   SIGATTN_ERR_LAYOUT = -9,        /* seq_lens and cu_seqlens both set for one axis */
-  SIGATTN_ERR_WORKSPACE = -10     /* workspace too small for the call, or misaligned */
+  SIGATTN_ERR_WORKSPACE = -10,    /* workspace too small for the call, or misaligned */
+  SIGATTN_ERR_SCRATCH = -11       /* sigattn_fwd_noalloc: scratch need above
+                                     SIGATTN_NOALLOC_SCRATCH_BYTES */
 };
 
 /*
@@ -121,6 +123,22 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
 size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p);
 int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
                    void *stream);
+
+/*
+ * sigattn_fwd_ws without a caller workspace and without any allocation
+ * (no counterpart in the reference): for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Split-KV problems keep their fp32 partials in a fixed
+ * device array inside the library, SIGATTN_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends; its address is looked up on the first call on
+ * each device (which must be current).  Every split plan fits (partials stay
+ * below 16 MiB); a larger need returns SIGATTN_ERR_SCRATCH.  Other problems
+ * run exactly as in sigattn_fwd.  Results equal sigattn_fwd_ws's bit for bit.
+ * All calls on one GPU share its array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ */
+#define SIGATTN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream);
 
 /*
  * Recompute backward: dq (q strides), dk and dv (k strides) from dout

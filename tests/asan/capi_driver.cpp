@@ -66,6 +66,11 @@ void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record(
 void launch_fwd_generic(const KParams &p, int, int, bool, hipStream_t) { record("fwd_generic", p); }
 void launch_bwd_dq_generic(const KParams &p, int, int, bool, hipStream_t) { record("dq_generic", p); }
 void launch_bwd_dkdv_generic(const KParams &p, int, int, bool, hipStream_t) { record("dkdv_generic", p); }
+// The fixed scratch of sigattn_fwd_noalloc: any aligned address stands in.
+hipError_t splitkv_scratch(float **ptr) {
+  *ptr = reinterpret_cast<float *>(uintptr_t(3) << 20);
+  return hipSuccess;
+}
 }  // namespace sigattn
 
 // The library maps hipGetLastError() after its launches; no launch happens here.
@@ -104,6 +109,7 @@ int main() {
     EXPECT(sigattn_check(&p) == b.code);
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == b.code);
     EXPECT(sigattn_fwd_ws(&p, kFake, kFake, 1 << 20, nullptr) == b.code);
+    EXPECT(sigattn_fwd_noalloc(&p, kFake, nullptr) == b.code);
     EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == b.code);
     EXPECT(sigattn_bwd_ws(&p, kFake, kFake, kFake, kFake, kFake, 1 << 20, nullptr) == b.code);
     EXPECT(sigattn_bwd_dq(&p, kFake, kFake, nullptr) == b.code);
@@ -125,7 +131,7 @@ int main() {
     EXPECT(sigattn_bwd_dq_ws(&p, kFake, nullptr, 1 << 20, nullptr) == SIGATTN_ERR_WORKSPACE);
     EXPECT(g_calls.empty());
   }
-  for (int code = -10; code <= 0; ++code) EXPECT(std::strlen(sigattn_strerror(code)) > 0);
+  for (int code = -11; code <= 0; ++code) EXPECT(std::strlen(sigattn_strerror(code)) > 0);
   EXPECT(std::strcmp(sigattn_strerror(-99), "unknown sigattn status") == 0);
 
   // --- dispatch of valid problems
@@ -176,6 +182,20 @@ int main() {
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_splitkv");
     EXPECT(g_last.nsplit == 1 && g_last.ws == nullptr);
     EXPECT(sigattn_fwd_ws(&p, kFake, kFake, ws - 1, nullptr) == SIGATTN_ERR_WORKSPACE && g_calls.empty());
+    // No allocation, no caller workspace: the partials go to the fixed scratch.
+    EXPECT(sigattn_fwd_noalloc(&p, kFake, nullptr) == 0 && calls() == "fwd_splitkv");
+    EXPECT(g_last.nsplit == 16 && g_last.ws == reinterpret_cast<float *>(uintptr_t(3) << 20));
+    // The largest split plan: one (batch, head) pair, 32 queries, D = 128.
+    p.Tq = 32;
+    p.Tk = 1 << 20;
+    p.k_stride_b = p.Tk * 128;
+    EXPECT(sigattn_fwd_workspace_bytes(&p) <= SIGATTN_NOALLOC_SCRATCH_BYTES);
+    EXPECT(sigattn_fwd_noalloc(&p, kFake, nullptr) == 0 && calls() == "fwd_splitkv");
+    EXPECT(g_last.nsplit == 512);
+    // A problem that does not split runs as sigattn_fwd does.
+    sigattn_problem d = base(2, 300, 3, 128);
+    EXPECT(sigattn_fwd_noalloc(&d, kFake, nullptr) == 0 && calls() == "fwd_mfma");
+    EXPECT(g_last.ws == nullptr && g_last.nsplit == 0);
   }
   {
     // Empty problems launch nothing.

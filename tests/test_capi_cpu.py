@@ -52,7 +52,7 @@ def test_abi_version_and_strerror():
     lib = _capi.load_library()
     assert lib.sigattn_abi_version() == _capi.ABI_VERSION
     assert lib.sigattn_strerror(0) == b"success"
-    for code in range(-10, 0):
+    for code in range(-11, 0):
         assert lib.sigattn_strerror(code) not in (b"", b"unknown sigattn status")
     assert lib.sigattn_strerror(-99) == b"unknown sigattn status"
 
@@ -96,6 +96,7 @@ def test_validation_error_codes(change, code):
     p = _problem(**change)
     assert lib.sigattn_check(ctypes.byref(p)) == code
     assert lib.sigattn_fwd(ctypes.byref(p), 1 << 20, None) == code
+    assert lib.sigattn_fwd_noalloc(ctypes.byref(p), 1 << 20, None) == code
     assert lib.sigattn_bwd(ctypes.byref(p), 1 << 20, 1 << 20, 1 << 20, 1 << 20, None) == code
 
 
@@ -106,6 +107,7 @@ def test_null_problem_and_null_outputs():
     p = _problem()
     assert lib.sigattn_check(ctypes.byref(p)) == 0
     assert lib.sigattn_fwd(ctypes.byref(p), None, None) == -1
+    assert lib.sigattn_fwd_noalloc(ctypes.byref(p), None, None) == -1
     assert lib.sigattn_bwd(ctypes.byref(p), 1 << 20, None, 1 << 20, 1 << 20, None) == -1
     assert lib.sigattn_bwd(ctypes.byref(p), None, 1 << 20, 1 << 20, 1 << 20, None) == -1
     assert lib.sigattn_bwd_dq(ctypes.byref(p), 1 << 20, None, None) == -1

@@ -150,11 +150,13 @@ const char *sigattn_strerror(int status) {
     case SIGATTN_ERR_DENSE_LENGTHS:
       return "dense attention (no seq_lens) requires the same sequence length for Q and K";
     case SIGATTN_ERR_ABI_VERSION: return "sigattn_problem.abi_version does not match the library";
-    case SIGATTN_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SIGATTN_ERR_LAUNCH: return "HIP kernel launch or HIP runtime call failed";
     case SIGATTN_ERR_LAYOUT:
       return "seq_lens and cu_seqlens cannot both be given for the same sequence axis";
     case SIGATTN_ERR_WORKSPACE:
       return "workspace too small for the call or not 16-byte aligned";
+    case SIGATTN_ERR_SCRATCH:
+      return "problem needs more than the fixed scratch buffer of sigattn_fwd_noalloc";
     default: return "unknown sigattn status";
   }
 }
@@ -197,8 +199,13 @@ size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p) {
   return (size_t)splitkv_workspace_bytes(p, splitkv_plan(p, use_mfma(p, none, 0)));
 }
 
-int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
-                   void *stream) {
+static_assert(sigattn::kSplitScratchBytes == SIGATTN_NOALLOC_SCRATCH_BYTES, "scratch size");
+
+// Forward: the split-KV partials go to `workspace` (caller memory), to the
+// library's fixed scratch array (static_scratch), or nowhere (one chunk per
+// (batch, head)).
+static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
+                    bool static_scratch, void *stream) {
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
   if (p->B == 0 || p->H == 0 || p->Tq == 0) return SIGATTN_OK;
@@ -209,7 +216,12 @@ int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t 
   const void *ptrs[4] = {p->q, p->k, p->v, out};
   const bool mfma = use_mfma(p, ptrs, 4);
   SplitPlan sp = splitkv_plan(p, mfma);
-  if (sp.nsplit > 1 && workspace != nullptr) {
+  if (sp.nsplit > 1 && static_scratch) {
+    if ((size_t)splitkv_workspace_bytes(p, sp) > sigattn::kSplitScratchBytes) return SIGATTN_ERR_SCRATCH;
+    float *ws = nullptr;
+    if (sigattn::splitkv_scratch(&ws) != hipSuccess) return SIGATTN_ERR_LAUNCH;
+    k.ws = ws;
+  } else if (sp.nsplit > 1 && workspace != nullptr) {
     if ((size_t)splitkv_workspace_bytes(p, sp) > workspace_bytes || !aligned16(workspace))
       return SIGATTN_ERR_WORKSPACE;
     k.ws = (float *)workspace;
@@ -230,8 +242,17 @@ int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t 
   return launch_status();
 }
 
+int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+  return fwd_impl(p, out, workspace, workspace_bytes, false, stream);
+}
+
 int sigattn_fwd(const sigattn_problem *p, void *out, void *stream) {
-  return sigattn_fwd_ws(p, out, nullptr, 0, stream);
+  return fwd_impl(p, out, nullptr, 0, false, stream);
+}
+
+int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream) {
+  return fwd_impl(p, out, nullptr, 0, true, stream);
 }
 
 // Which kernels a backward call runs.

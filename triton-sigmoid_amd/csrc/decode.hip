@@ -20,10 +20,50 @@
 // key against 4·D·32 MFMA FLOPs), so each block is computed as a plain
 // sequence: Sᵀ = K·Qᵀ, P = sigmoid(Sᵀ) on packed words, Oᵀ += Vᵀ·Pᵀ.  The four
 // waves' Oᵀ partials are summed through LDS at the end.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
 namespace sigattn {
+
+// Partials of sigattn_fwd_noalloc's split-KV launches.  In host code the name
+// `scratch` is only a stand-in for the symbol: its device address (one per
+// GPU) comes from hipGetSymbolAddress and is what kernels are given.  Every
+// call on a GPU uses that GPU's one array, so calls that overlap on one GPU
+// (two streams, two threads) race.  No clearing is needed: the reduction reads
+// exactly the partials the chunk kernel of the same call writes.
+static __device__ __align__(256) float scratch[kSplitScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float *> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+hipError_t splitkv_scratch(float **ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  float *p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    // First call on this device (which is current): look the address up.
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void *addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (addr == nullptr) return hipErrorInvalidSymbol;
+      p = static_cast<float *>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return hipSuccess;
+}
 
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

@@ -28,6 +28,17 @@ void launch_bwd_dq_ds_mfma(const KParams &p, int dtype, int D, bool causal, hipS
 // nsplit * B * H * Tq * D floats when nsplit > 1.
 void launch_fwd_splitkv(const KParams &p, int dtype, int D, bool scoremod, hipStream_t st);
 
+// Fixed device scratch of the split-KV forward for callers that cannot
+// allocate (sigattn_fwd_noalloc): a file-scope __device__ array of this many
+// bytes in decode.hip, one per GPU, held until the process ends.  The split
+// plan never needs more: fp32 partials of nsplit * B * H * Tq * D floats with
+// nsplit * B * H < 1024 (splitting stops at 512 (batch, head) pairs), Tq <= 32
+// and D <= 128 stay below 16 MiB.
+constexpr size_t kSplitScratchBytes = size_t(16) << 20;
+// Device address of the current device's scratch array (looked up once per
+// device with hipGetSymbolAddress); hipSuccess or the lookup's error.
+hipError_t splitkv_scratch(float **ptr);
+
 // Portable kernels: any dtype, D in {16, 32, 64, 128}, any alignment.
 void launch_fwd_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
 void launch_bwd_dq_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);

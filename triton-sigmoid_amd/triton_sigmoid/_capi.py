@@ -66,6 +66,7 @@ SIGNATURES = {
     "sigattn_fwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp], _c_i32),
     "sigattn_fwd_workspace_bytes": ([ctypes.POINTER(SigattnProblem)], ctypes.c_size_t),
     "sigattn_fwd_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, ctypes.c_size_t, _c_vp], _c_i32),
+    "sigattn_fwd_noalloc": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp], _c_i32),
     "sigattn_bwd": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dq": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp], _c_i32),
     "sigattn_bwd_dkdv": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp], _c_i32),
