@@ -30,6 +30,7 @@ import itertools
 import json
 import math
 import os
+import re
 import statistics
 import sys
 import time
@@ -310,6 +311,90 @@ def kernel_source_digest() -> str:
     return h.hexdigest()[:16]
 
 
+def _pmc_rows(path: str, counter: str) -> dict:
+    """{kernel name: [value per dispatch]} of one counter from a rocprofv3
+    --pmc csv (<dir>/<name>_counter_collection.csv)."""
+    import csv
+    out: dict = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def traffic_json(config: str, fetch_csv: str, write_csv: str, cal_fetch_csv: str, cal_write_csv: str) -> dict:
+    """profiles/hbm_traffic.json from four rocprofv3 --pmc runs: FETCH_SIZE and
+    WRITE_SIZE of `bench.py --config <config> --kernels dense`, and the same two
+    counters of `bench.py --copy-calibration` (one 1 GiB device copy).  Bytes
+    per launch = counter KiB x 1024 x (1 GiB / the copy's reading of it); the
+    median over the dispatches of each kernel.  Records the kernel-source
+    digest, so bench.py reports the traffic only for these kernels."""
+    cfg = CONFIGS[config]
+    one_gib = float(1 << 30)
+    def copy_kib(path, counter):
+        rows = [v for k, vs in _pmc_rows(path, counter).items() if "copyBuffer" in k for v in vs]
+        if not rows:
+            raise SystemExit(f"{path}: no {counter} row of the calibration copy (__amd_rocclr_copyBuffer)")
+        return statistics.median(rows)
+
+    fcal, wcal = copy_kib(cal_fetch_csv, "FETCH_SIZE"), copy_kib(cal_write_csv, "WRITE_SIZE")
+    ffac, wfac = one_gib / (fcal * 1024), one_gib / (wcal * 1024)
+    fetch, write = _pmc_rows(fetch_csv, "FETCH_SIZE"), _pmc_rows(write_csv, "WRITE_SIZE")
+    B, L, H, D = cfg["B"], cfg["L"], cfg["H"], cfg["D"]
+    tensor = B * L * H * D * 2
+    nqb = -(-L // 32)
+    ds_tiles = nqb * (nqb + 1) // 2 if cfg["causal"] else nqb * nqb
+    ds_bytes = B * H * ds_tiles * 2048 if D == 128 else 0
+    algo = {"fwd": 4 * tensor, "bwd_dkdv": 6 * tensor + ds_bytes,
+            "bwd_dq": (2 * tensor + ds_bytes) if ds_bytes else 5 * tensor}
+    out = {"src_digest": kernel_source_digest(), "config": config,
+           "calibration": {"copy_bytes": int(one_gib), "fetch_kib": fcal, "write_kib": wcal,
+                           "fetch_factor": round(ffac, 4), "write_factor": round(wfac, 4)}}
+    entry = {}
+    for name in ("fwd", "bwd_dkdv", "bwd_dq"):
+        fks = [(k, vs) for k, vs in fetch.items() if _kernel_matches(name, k)]
+        wks = [(k, vs) for k, vs in write.items() if _kernel_matches(name, k)]
+        if not fks or not wks:
+            continue
+        fk = statistics.median(v for _, vs in fks for v in vs)
+        wk = statistics.median(v for _, vs in wks for v in vs)
+        nbytes = fk * 1024 * ffac + wk * 1024 * wfac
+        entry[name] = {"kernel": _kernel_base(fks[0][0]), "bytes_per_launch": int(nbytes),
+                       "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
+                       "algorithmic_bytes": int(algo[name]), "ratio": round(nbytes / algo[name], 3)}
+    out[config] = entry
+    return out
+
+
+# Function names of the kernels bench.py times under each name (rocprofv3
+# reports some kernel names mangled, some demangled, so they are searched for).
+_KERNEL_NAMES = {
+    "fwd": ("fwd_mfma_kernel", "fwd_splitkv_kernel", "fwd_generic_kernel"),
+    "bwd_dkdv": ("bwd_dkdv_pair_kernel", "bwd_dkdv_kernel", "dkdv_generic_kernel"),
+    "bwd_dq": ("bwd_dq_ds_kernel", "bwd_dq_kernel", "dq_generic_kernel"),
+}
+
+
+def _kernel_base(kernel: str):
+    """The library kernel function a profiled kernel name refers to
+    ('_ZN7sigattn15fwd_mfma_kernelI...' or 'void sigattn::fwd_mfma_kernel<...>(...)'),
+    or None for other kernels."""
+    m = re.match(r"_ZN7sigattn(\d+)", kernel)
+    if m:
+        name = kernel[m.end():m.end() + int(m.group(1))]
+    else:
+        m = re.search(r"sigattn::(\w+)", kernel)
+        name = m.group(1) if m else None
+    return name if any(name in names for names in _KERNEL_NAMES.values()) else None
+
+
+def _kernel_matches(name: str, kernel: str) -> bool:
+    """Whether a profiled kernel is one bench.py times as `name`."""
+    return _kernel_base(kernel) in _KERNEL_NAMES[name]
+
+
 def load_traffic(kernel: str, config: str):
     """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc FETCH_SIZE
     and WRITE_SIZE (scaled by the copy calibration), from
@@ -485,7 +570,19 @@ def main():
                     help="split-KV forward at decode shapes (HBM GB/s)")
     ap.add_argument("--ceiling", action="store_true",
                     help="hipBLASLt bf16 GEMM TFLOPS on random and on zero operands (the box's practical MFMA rate)")
+    ap.add_argument("--kernels", choices=("dense", "padded", "packed"),
+                    help="only time the config's kernels through the C ABI in this layout (a program to "
+                         "profile: no API steps, no CPU baseline)")
+    ap.add_argument("--traffic-json", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
+                    help="write profiles/hbm_traffic.json for --config from rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE csvs of `--kernels dense` and of `--copy-calibration`")
     args = ap.parse_args()
+    if args.traffic_json:
+        data = traffic_json(args.config, *args.traffic_json)
+        path = ROOT / "profiles" / "hbm_traffic.json"
+        path.write_text(json.dumps(data, indent=1) + "\n")
+        print(json.dumps(data), flush=True)
+        return
     if args.ceiling:
         print(json.dumps({"metric": "practical MFMA rate (bf16 GEMM)", "unit": "TFLOPS", **mfma_ceiling()}),
               flush=True)
@@ -514,6 +611,15 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.kernels:
+        cfg = CONFIGS[args.config]
+        q, k, v, do = make_inputs(cfg, dev)
+        sl = make_seq_lens(cfg, dev) if args.kernels != "dense" else None
+        if args.kernels != "dense" and sl is None:
+            sys.exit(f"--kernels {args.kernels} needs a padded config")
+        kt = kernel_times(cfg, q, k, v, do, iters=args.steps, seq_lens=sl, packed=args.kernels == "packed")
+        print(json.dumps({"config": args.config, "layout": args.kernels, "kernel_ms": kt}), flush=True)
+        return
     res = measure_config(args.config, args.steps, args.warmup)
     B, L, H, D, causal = (res["cfg"][n] for n in ("B", "L", "H", "D", "causal"))
     kt, P, dominant = res["kernel_ms"], res["pairs"], res["dominant"]

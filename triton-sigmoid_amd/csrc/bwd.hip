@@ -57,6 +57,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   }
   const int Lq = p.len_q(b);
   const int Lk = p.len_k(b);
+  // Padding item: its zero rows as part of one contiguous span (see zero_row_span).
+  if (qb * BM >= Lq && p.q_rows_contiguous(D)) {
+    zero_row_span((uint16_t *)p.dq + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
+                  threadIdx.x, 256);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -264,6 +270,13 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   }
   const int Lq = p.len_q(b);
   const int Lk = p.len_k(b);
+  // Padding item: its zero dK and dV rows as part of contiguous spans (see zero_row_span).
+  if (kblk * BN >= Lk && p.k_rows_contiguous(D)) {
+    const int r1 = min(kblk * BN + BN, p.Tk);
+    zero_row_span((uint16_t *)p.dk + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 256);
+    zero_row_span((uint16_t *)p.dv + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 256);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -627,6 +640,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
     if (item > 0) __syncthreads();
     const int Lq = p.len_q(b);
     const int Lk = p.len_k(b);
+    // Padding item (ragged batches, one key block per workgroup): its zero
+    // dK and dV rows as part of contiguous spans (see zero_row_span).
+    if (nitems == 1 && kblk * BN >= Lk && p.k_rows_contiguous(D)) {
+      const int r1 = min(kblk * BN + BN, p.Tk);
+      zero_row_span((uint16_t *)p.dk + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 512);
+      zero_row_span((uint16_t *)p.dv + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 512);
+      return;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -995,6 +1016,12 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) 
   }
   const int Lq = p.len_q(b);
   const int Lk = p.len_k(b);
+  // Padding item: its zero rows as part of one contiguous span (see zero_row_span).
+  if (qblk * BM >= Lq && p.q_rows_contiguous(D)) {
+    zero_row_span((uint16_t *)p.dq + (int64_t)b * p.sq_b, p.sq_t, qblk * BM, min(qblk * BM + BM, p.Tq), h,
+                  p.H, threadIdx.x, 64 * NW);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);

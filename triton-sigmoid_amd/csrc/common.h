@@ -121,7 +121,32 @@ struct KParams {
   __host__ __device__ __forceinline__ bool ragged() const {
     return seq_q != nullptr || seq_k != nullptr || cu_q != nullptr || cu_k != nullptr;
   }
+  // Padded layout whose rows hold every head back to back (row stride H*D,
+  // head stride D), so the rows of a row block over all heads are one
+  // contiguous span of the Q-shaped / K-shaped tensors.
+  __device__ __forceinline__ bool q_rows_contiguous(int D) const {
+    return cu_q == nullptr && sq_h == D && sq_t == (int64_t)H * D;
+  }
+  __device__ __forceinline__ bool k_rows_contiguous(int D) const {
+    return cu_k == nullptr && sk_h == D && sk_t == (int64_t)H * D;
+  }
 };
+
+// Zero rows of the padded layout.  A row block wholly past a batch's valid
+// length is a padding work item for each of the H heads; when every head's
+// rows are contiguous (KParams::q_rows_contiguous / k_rows_contiguous), the
+// rows [row0, row1) of all heads form one span of (row1 - row0) * row_elems
+// elements at batch_base + row0 * row_elems, and the item of head `part` of
+// `nparts` zeroes its 1/nparts of it with contiguous 16-byte stores (rather
+// than its own head's rows, 2*D bytes at a stride of 2*H*D).  row_elems is a
+// multiple of 8 and batch_base 16-byte aligned (MFMA-path requirements).
+__device__ __forceinline__ void zero_row_span(void *batch_base, int64_t row_elems, int row0, int row1,
+                                              int part, int nparts, int tid, int nthreads) {
+  const int64_t n = (int64_t)(row1 - row0) * row_elems / 8;  // 16-byte pieces
+  const int64_t c0 = n * part / nparts, c1 = n * (part + 1) / nparts;
+  u32x4 *dst = (u32x4 *)((uint16_t *)batch_base + (int64_t)row0 * row_elems);
+  for (int64_t c = c0 + tid; c < c1; c += nthreads) dst[c] = (u32x4){0u, 0u, 0u, 0u};
+}
 
 // ---------------------------------------------------------------------------
 // Work-item order.  A kernel's grid covers (row block, batch, head) items of

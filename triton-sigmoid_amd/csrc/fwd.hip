@@ -32,14 +32,23 @@
 
 namespace sigattn {
 
+// LDS ring stages of the D = 64 forward: three (48 KB) let three workgroups
+// share a CU, four (64 KB) two.
+#ifndef SIGATTN_FWD_D64_STAGES
+#define SIGATTN_FWD_D64_STAGES 3
+#endif
+
+template <int D> constexpr int fwd_stages() { return D == 64 ? SIGATTN_FWD_D64_STAGES : 4; }
+template <int D> constexpr int fwd_occupancy() { return D == 64 ? (fwd_stages<D>() == 3 ? 3 : 2) : 1; }
+
 template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(64 * NWV, (D == 64 ? 3 : 1)) void fwd_mfma_kernel(const KParams p) {
+__global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(const KParams p) {
   // NWV waves per workgroup (8: two per SIMD), NCB 32-query column blocks each.
   constexpr int QW = 32 * NCB;          // queries per wave
   constexpr int BM = NWV * QW;          // queries per workgroup
   constexpr int BN = 64;                // keys per LDS tile (two 32-key blocks)
   // LDS ring stages: D = 64 uses three (48 KB), so three workgroups share a CU.
-  constexpr int NST = D == 64 ? 3 : 4;
+  constexpr int NST = fwd_stages<D>();
   constexpr int NKS = D / 16;           // MFMA k-steps over the head dim
   constexpr int NDB = D / 32;           // 32-row blocks of Oᵀ
   constexpr int NSTEP = NKS + 2 * NDB;  // steps (NCB MFMAs sharing an A operand) per region
@@ -73,6 +82,13 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 ? 3 : 1)) void fwd_mfma_kernel(c
 
   const int Lq = p.len_q(b);
   const int Lk = p.len_k(b);
+  // Padding item (the row block lies wholly past seq_lens_q): its zero rows
+  // as part of one contiguous span over all heads when the layout allows.
+  if (qb * BM >= Lq && p.q_rows_contiguous(D)) {
+    zero_row_span((uint16_t *)p.out + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
+                  threadIdx.x, 64 * NWV);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);

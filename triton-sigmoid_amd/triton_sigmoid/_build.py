@@ -43,32 +43,49 @@ def compile_flags() -> list[str]:
     ]
 
 
-def _compile(src: Path, obj: Path) -> None:
+def _compile(src: Path, obj: Path, defines: tuple = ()) -> None:
     lang = ["-x", "hip"] if src.suffix == ".cpp" else []
-    cmd = [hipcc(), *compile_flags(), *lang, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *compile_flags(), *defines, *lang, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
 
 
-def build(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compiles every source and links LIB_PATH.  Always rebuilds."""
-    BUILD_DIR.mkdir(exist_ok=True)
-    objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
+def build(verbose: bool = False, jobs: int = 4, defines: tuple = (), out: Path | None = None) -> Path:
+    """Compiles every source and links LIB_PATH (or `out`).  Always rebuilds.
+
+    `defines` are extra -D options for the tile-configuration macros of the
+    kernel sources (e.g. "-DSIGATTN_FWD_D64_STAGES=4"); a build with them
+    goes to `out` (its objects to a folder of their own), and _capi loads it
+    when the environment variable SIGATTN_LIBRARY names it."""
+    defines = tuple(defines)
+    if defines and out is None:
+        raise ValueError("a build with extra defines needs its own output path")
+    lib = Path(out) if out is not None else LIB_PATH
+    bdir = BUILD_DIR if not defines else BUILD_DIR / ("variant_" + lib.stem)
+    bdir.mkdir(parents=True, exist_ok=True)
+    objs = [bdir / (Path(s).stem + ".o") for s in SOURCES]
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, CSRC / s, o) for s, o in zip(SOURCES, objs)]
+        futs = [ex.submit(_compile, CSRC / s, o, defines) for s, o in zip(SOURCES, objs)]
         for f in futs:
             f.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    import argparse
+
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--out", type=Path, help="output library (required with -D options)")
+    args, defines = ap.parse_known_args()
+    if any(not d.startswith("-D") for d in defines):
+        ap.error(f"unknown arguments {defines}")
+    build(verbose=True, defines=tuple(defines), out=args.out)

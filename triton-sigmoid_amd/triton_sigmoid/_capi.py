@@ -16,7 +16,10 @@ from typing import Optional
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libsigattn.so"
+# The library built next to this file; the environment variable
+# SIGATTN_LIBRARY may name another build of the same sources (a tile-
+# configuration variant from _build.py --out ... -D...).
+LIB_PATH = Path(os.environ.get("SIGATTN_LIBRARY") or Path(__file__).resolve().parent / "libsigattn.so")
 ABI_VERSION = 2
 
 F16, BF16, F32 = 0, 1, 2
@@ -315,6 +318,40 @@ def forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) 
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
     _launch_fwd(lib, pr, out)
     return out
+
+
+def forward_eager(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):
+    """forward() for the eager autograd paths.  Also returns the launched
+    problem when it points at exactly the tensors given (none needed a copy
+    or conversion), which the caller saves for the backward; backward_eager
+    then launches on it without validating and describing the problem a
+    second time.  Otherwise the problem is None."""
+    lib = load_library()
+    given = (Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
+    canon = _prepare(*given)
+    out = torch.empty_like(canon[0])
+    if out.numel() == 0:
+        return out, None
+    pr = _problem(*canon, causal)
+    _launch_fwd(lib, pr, out)
+    return out, (pr if all(a is b for a, b in zip(given, canon)) else None)
+
+
+def backward_eager(pr, Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):
+    """backward() on the problem forward_eager returned for the same saved
+    tensors (which keep every pointer in it alive), or backward() itself
+    when there is none."""
+    if pr is None:
+        return backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
+    lib = load_library()
+    dO = _as(dO, Q.dtype, Q.device)
+    if dO.shape != Q.shape:
+        raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
+    dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    if dQ.numel() == 0 and dK.numel() == 0:
+        return dQ, dK, dV
+    _launch_bwd(lib, pr, dO, dQ, dK, dV)
+    return dQ, dK, dV
 
 
 def backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):

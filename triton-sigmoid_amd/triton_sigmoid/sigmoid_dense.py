@@ -98,7 +98,7 @@ class _DenseEager(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, Q, K, V, bias, score_mod, sm_scale, is_causal):
-        out = _capi.forward(Q, K, V, bias, score_mod, sm_scale, None, None, is_causal)
+        out, ctx.problem = _capi.forward_eager(Q, K, V, bias, score_mod, sm_scale, None, None, is_causal)
         _dense_setup_context(ctx, (Q, K, V, bias, score_mod, sm_scale, is_causal), out)
         return out
 
@@ -109,7 +109,8 @@ class _DenseEager(torch.autograd.Function):
         else:
             Q, K, V, bias, sm_scale = ctx.saved_tensors
             score_mod = None
-        dQ, dK, dV = _capi.backward(Q, K, V, dO, bias, score_mod, sm_scale, None, None, ctx.is_causal)
+        dQ, dK, dV = _capi.backward_eager(ctx.problem, Q, K, V, dO, bias, score_mod, sm_scale, None, None,
+                                          ctx.is_causal)
         return dQ, dK, dV, None, None, None, None
 
 

@@ -100,7 +100,8 @@ class _PaddedEager(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, Q, K, V, seq_lens_k, seq_lens_q, bias, score_mod, sm_scale, is_causal):
-        out = _capi.forward(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, is_causal)
+        out, ctx.problem = _capi.forward_eager(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k,
+                                               is_causal)
         _padded_setup_context(ctx, (Q, K, V, seq_lens_k, seq_lens_q, bias, score_mod, sm_scale, is_causal), out)
         return out
 
@@ -109,8 +110,8 @@ class _PaddedEager(torch.autograd.Function):
         saved = ctx.saved_tensors
         Q, K, V, seq_lens_k, seq_lens_q, bias, sm_scale = saved[:7]
         score_mod = saved[7] if ctx.has_score_mod else None
-        dQ, dK, dV = _capi.backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k,
-                                    ctx.is_causal)
+        dQ, dK, dV = _capi.backward_eager(ctx.problem, Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q,
+                                          seq_lens_k, ctx.is_causal)
         return dQ, dK, dV, None, None, None, None, None, None
 
 
