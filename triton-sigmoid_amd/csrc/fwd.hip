@@ -39,6 +39,16 @@ namespace sigattn {
 #endif
 
 template <int D> constexpr int fwd_stages() { return D == 64 ? SIGATTN_FWD_D64_STAGES : 4; }
+
+// Dense causal grids pair query blocks (j, nblk-1-j) in one workgroup, in
+// the XCD-grouped order (every workgroup equal; K / V of a (batch, head) read
+// by its workgroups while they sit in one L2).  Off: measured 2-3 % slower
+// at B=4 L=4096 H=16 D=128 and 26 % at B=2 L=1024 H=8 D=64 (half the
+// workgroups) than one block per workgroup, heaviest first.
+#ifndef SIGATTN_FWD_CAUSAL_PAIRS
+#define SIGATTN_FWD_CAUSAL_PAIRS 0
+#endif
+constexpr bool kFwdCausalPairs = SIGATTN_FWD_CAUSAL_PAIRS != 0;
 template <int D> constexpr int fwd_occupancy() { return D == 64 ? (fwd_stages<D>() == 3 ? 3 : 2) : 1; }
 
 template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
@@ -65,315 +75,333 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sV[NST][BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? NST * BN : 4];
 
-  int b, h, qb;
+  int b, h, qb0, nitems = 1;
   if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
                                : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
-    b = it.b, h = it.h, qb = it.blk;
+    b = it.b, h = it.h, qb0 = it.blk;
   } else {
     const int BH = p.B * p.H;
     int bh;
-    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb);
-    if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
+    if (CAUSAL && kFwdCausalPairs) {
+      // Query blocks nblk-1-j and j in sequence (grid = ceil(nblk/2) per
+      // (batch, head)): under the causal mask the two together stream
+      // nblk+1 key blocks' worth for every j, so all workgroups are equal and
+      // the XCD-grouped order (K and V of a (batch, head) read by its
+      // workgroups while they sit in one L2) costs no balance.
+      int j;
+      dense_item(blockIdx.x, BH, (p.nblk + 1) / 2, true, bh, j);
+      qb0 = p.nblk - 1 - j;
+      nitems = j < qb0 ? 2 : 1;
+    } else {
+      dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb0);
+      if (CAUSAL) qb0 = p.nblk - 1 - qb0;  // heaviest query blocks first
+    }
     b = bh / p.H, h = bh % p.H;
   }
 
-  const int Lq = p.len_q(b);
-  const int Lk = p.len_k(b);
-  // Padding item (the row block lies wholly past seq_lens_q): its zero rows
-  // as part of one contiguous span over all heads when the layout allows.
-  if (qb * BM >= Lq && p.q_rows_contiguous(D)) {
-    zero_row_span((uint16_t *)p.out + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
-                  threadIdx.x, 64 * NWV);
-    return;
-  }
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int q0 = qb * BM;
-  // Query slot of the wave.  With eight waves, waves w and w+4 share a SIMD;
-  // giving them complementary slots (w and 7-w) evens out the per-SIMD work of
-  // causal diagonal workgroups once waves stop at their own last key block.
-  const int slot = (NWV == 8 && w >= 4) ? 11 - w : w;
-  const int qw = q0 + slot * QW;    // this wave's first query
-  const int myq0 = qw + l32;        // this lane's query in column block 0 (block c: +32c)
-
-  const int64_t qoff = p.q_base(b, h), koff = p.k_base(b, h);
-  const uint16_t *Qb = (const uint16_t *)p.q + qoff;
-  const uint16_t *Kb = (const uint16_t *)p.k + koff;
-  const uint16_t *Vb = (const uint16_t *)p.v + koff;
-  uint16_t *Ob = (uint16_t *)p.out + qoff;
-
-  int nend = Lk;
-  if (CAUSAL) nend = min(nend, min(q0 + BM, Lq));
-  if (q0 >= Lq) nend = 0;
-  const int ntiles = (nend + BN - 1) / BN;
-  const int NB = 2 * ntiles;  // 32-key blocks of the workgroup
-
-  const float scale = *p.scale;
-  const float bias = p.bias[b];
-  const float nsl = -scale * kLog2e;
-  const float nbl = -bias * kLog2e;
-
-  // This wave's query rows as B operands (k = d = 16s + 8h + j).
-  u32x4 qf[NCB][NKS];
-#pragma unroll
-  for (int c = 0; c < NCB; ++c) {
-    const int q = myq0 + 32 * c;
-    const bool ok = q < Lq;
-    const uint16_t *qrow = Qb + (int64_t)q * p.sq_t + 8 * hi;
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) qf[c][s] = ok ? *(const u32x4 *)(qrow + 16 * s) : zero4();
-  }
-  // Consume the Q loads here, so the compiler's wait for them is not placed
-  // at the head of the key loop, where it would also wait for the tile copies.
-#pragma unroll
-  for (int c = 0; c < NCB; ++c)
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(qf[c][s]));
-
-  f32x16 acc[NCB][NDB];
-#pragma unroll
-  for (int c = 0; c < NCB; ++c)
-#pragma unroll
-    for (int d = 0; d < NDB; ++d) acc[c][d] = zero16();
-
-  TileOffsets<D> to;
-  to.init(lane);
-  DmaPlan<BN, D, NWV> dma;
-  dma.init(w, lane);
-  const int kv_stride_bytes = (int)(p.sk_t * 2);
-
-  float creg = 0.0f;
-  auto load_c = [&](int n0) SIGATTN_INLINE {
-    if (SCOREMOD && tid < BN) {
-      const int key = n0 + tid;
-      creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
+#pragma clang loop unroll(disable)
+  for (int item = 0; item < nitems; ++item) {
+    const int qb = item == 0 ? qb0 : p.nblk - 1 - qb0;
+    // The previous item's last LDS reads precede this item's tile fills.
+    if (item > 0) __syncthreads();
+    const int Lq = p.len_q(b);
+    const int Lk = p.len_k(b);
+    // Padding item (the row block lies wholly past seq_lens_q): its zero rows
+    // as part of one contiguous span over all heads when the layout allows.
+    if (qb * BM >= Lq && nitems == 1 && p.q_rows_contiguous(D)) {
+      zero_row_span((uint16_t *)p.out + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
+                    threadIdx.x, 64 * NWV);
+      return;
     }
-  };
-  auto issue = [&](int st, int t) SIGATTN_INLINE {
-    load_c(t * BN);
-    dma.issue(sK[st], Kb, kv_stride_bytes, t * BN, Lk);
-    dma.issue(sV[st], Vb, kv_stride_bytes, t * BN, Lk);
-  };
 
-  // A operand of step o of the region whose S block sits at tile rows kl of
-  // stage stc and whose Oᵀ block sits at the same rows of stage stv: steps
-  // 0..NKS-1 are K rows (k-step o), the rest Vᵀ operands (16-key step j,
-  // 32-row block db).
-  auto read_op = [&](int o, int stc, int stv, int kl) SIGATTN_INLINE {
-    if (o < NKS) return ld_row<D>(sK[stc], to, kl, o);
-    const int i = o - NKS, j = i / NDB, db = i % NDB;
-    return ld_tr<D>(sV[stv], to, kl / 16 + j, db);
-  };
-  // Block g needs element masks when it crosses seq_lens_k or the diagonal of
-  // this wave's first query.
-  auto needs_mask = [&](int g) SIGATTN_INLINE {
-    return (32 * g + 32 > Lk) || (CAUSAL && 32 * g + 31 > qw);
-  };
-  // Zeroes the P entries of block g whose key lies before 0 (pipeline fill),
-  // at or past seq_lens_k, or after the lane's query.  Works on the packed
-  // words, so garbage scores of such keys never matter.
-  auto mask_words = [&](uint32_t (&pk)[NCB][8], int g) SIGATTN_INLINE {
-    int kbase = 32 * g;
-    asm volatile("" : "+s"(kbase));  // keeps this rare fix-up in its own branch
-#pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-      const unsigned lim = CAUSAL ? (unsigned)min(Lk, myq0 + 32 * cb + 1) : (unsigned)Lk;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 2 * e;
-        const unsigned k0 = (unsigned)(kbase + 8 * (i / 4) + 4 * hi + (i % 4));
-        const uint32_t m = (k0 < lim ? 0x0000ffffu : 0u) | (k0 + 1u < lim ? 0xffff0000u : 0u);
-        pk[cb][e] &= m;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int q0 = qb * BM;
+    // Query slot of the wave.  With eight waves, waves w and w+4 share a SIMD;
+    // giving them complementary slots (w and 7-w) evens out the per-SIMD work of
+    // causal diagonal workgroups once waves stop at their own last key block.
+    const int slot = (NWV == 8 && w >= 4) ? 11 - w : w;
+    const int qw = q0 + slot * QW;    // this wave's first query
+    const int myq0 = qw + l32;        // this lane's query in column block 0 (block c: +32c)
+
+    const int64_t qoff = p.q_base(b, h), koff = p.k_base(b, h);
+    const uint16_t *Qb = (const uint16_t *)p.q + qoff;
+    const uint16_t *Kb = (const uint16_t *)p.k + koff;
+    const uint16_t *Vb = (const uint16_t *)p.v + koff;
+    uint16_t *Ob = (uint16_t *)p.out + qoff;
+
+    int nend = Lk;
+    if (CAUSAL) nend = min(nend, min(q0 + BM, Lq));
+    if (q0 >= Lq) nend = 0;
+    const int ntiles = (nend + BN - 1) / BN;
+    const int NB = 2 * ntiles;  // 32-key blocks of the workgroup
+
+    const float scale = *p.scale;
+    const float bias = p.bias[b];
+    const float nsl = -scale * kLog2e;
+    const float nbl = -bias * kLog2e;
+
+    // This wave's query rows as B operands (k = d = 16s + 8h + j).
+    u32x4 qf[NCB][NKS];
+  #pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+      const int q = myq0 + 32 * c;
+      const bool ok = q < Lq;
+      const uint16_t *qrow = Qb + (int64_t)q * p.sq_t + 8 * hi;
+  #pragma unroll
+      for (int s = 0; s < NKS; ++s) qf[c][s] = ok ? *(const u32x4 *)(qrow + 16 * s) : zero4();
+    }
+    // Consume the Q loads here, so the compiler's wait for them is not placed
+    // at the head of the key loop, where it would also wait for the tile copies.
+  #pragma unroll
+    for (int c = 0; c < NCB; ++c)
+  #pragma unroll
+      for (int s = 0; s < NKS; ++s) asm volatile("" ::"v"(qf[c][s]));
+
+    f32x16 acc[NCB][NDB];
+  #pragma unroll
+    for (int c = 0; c < NCB; ++c)
+  #pragma unroll
+      for (int d = 0; d < NDB; ++d) acc[c][d] = zero16();
+
+    TileOffsets<D> to;
+    to.init(lane);
+    DmaPlan<BN, D, NWV> dma;
+    dma.init(w, lane);
+    const int kv_stride_bytes = (int)(p.sk_t * 2);
+
+    float creg = 0.0f;
+    auto load_c = [&](int n0) SIGATTN_INLINE {
+      if (SCOREMOD && tid < BN) {
+        const int key = n0 + tid;
+        creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
       }
-    }
-  };
+    };
+    auto issue = [&](int st, int t) SIGATTN_INLINE {
+      load_c(t * BN);
+      dma.issue(sK[st], Kb, kv_stride_bytes, t * BN, Lk);
+      dma.issue(sV[st], Vb, kv_stride_bytes, t * BN, Lk);
+    };
 
-  f32x16 sbuf[2][NCB];        // Sᵀ accumulators, by block parity
-  uint32_t pbuf[2][NCB][8];   // packed P words, by block parity
-  u32x4 opq[LA];              // A operands of the next LA steps (slot = step % LA)
-  float ea[2];                // exp2 terms of the next word (sigmoid stage A)
-
-  // Region r (U = r mod 8, so every slot and ring stage is static):
-  //   MFMA: Sᵀ(r) = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ(r-2), one step = NCB MFMAs (one per
-  //         column block) sharing an A operand read LA steps earlier;
-  //   VALU: P(r-1) = sigmoid(Sᵀ(r-1)) as a two-stage pipeline over packed
-  //         words (exp2 of the next word, then reciprocal and packing);
-  //   LDS:  the operand LA steps ahead (wrapping into region r+1).
-  // Block g lives in tile g/2 (rows 32*(g%2)) in ring stage (g/2)%4.  In odd
-  // regions r = 2u-1, step BAR publishes tile u (its first read, the K rows of
-  // block r+1, comes next) and starts the copy of tile u+1 into the stage of
-  // tile u+1-NST.  With four stages that tile's last reads were issued two
-  // regions earlier, so the barrier needs no wait for this wave's own LDS
-  // reads; with three (D = 64) they were issued in this region, and every
-  // wave waits for them before the barrier.
-  auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
-    constexpr int U = decltype(u_tag)::value;
-    constexpr int SL = U % 2;                    // parity of blocks r and r-2
-    constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
-    constexpr int STC = (U / 2) % NST;           // stage of block r
-    constexpr int STV = ((U + 2 * NST - 2) / 2) % NST;  // stage of block r-2
-    constexpr int STCn = ((U + 1) / 2) % NST;    // stage of block r+1
-    constexpr int STVn = ((U + 2 * NST - 1) / 2) % NST;  // stage of block r-1
-    f32x16(&sc)[NCB] = sbuf[SL];
-    const f32x16(&sp)[NCB] = sbuf[1 - SL];
-    uint32_t(&pn)[NCB][8] = pbuf[1 - SL];
-    const uint32_t(&pp)[NCB][8] = pbuf[SL];
-    float c[16];   // exp2 offsets of block r-1 (per key row)
-    float cn[2];   // ... of block r's first word
-    if constexpr (SCOREMOD) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 cv = *(const float4 *)&sC[STVn * BN + KLn + 8 * g + 4 * hi];
-        c[4 * g + 0] = cv.x; c[4 * g + 1] = cv.y; c[4 * g + 2] = cv.z; c[4 * g + 3] = cv.w;
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) cn[i] = sC[STC * BN + KL + 4 * hi + i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) c[i] = nbl;
-      cn[0] = cn[1] = nbl;
-    }
-#pragma unroll
-    for (int step = 0; step < NSTEP; ++step) {
-      if ((U % 2) == 1 && step == BAR) {
-        const int u = (r + 1) / 2;
-        if (u < ntiles) {
-          wait_dma();
-          if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
-          // With three stages the copy below refills the stage this region's
-          // Vᵀ operands came from: every wave's reads of it complete first.
-          if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-          if (u + 1 < ntiles) issue((u + 1) % NST, u + 1);
+    // A operand of step o of the region whose S block sits at tile rows kl of
+    // stage stc and whose Oᵀ block sits at the same rows of stage stv: steps
+    // 0..NKS-1 are K rows (k-step o), the rest Vᵀ operands (16-key step j,
+    // 32-row block db).
+    auto read_op = [&](int o, int stc, int stv, int kl) SIGATTN_INLINE {
+      if (o < NKS) return ld_row<D>(sK[stc], to, kl, o);
+      const int i = o - NKS, j = i / NDB, db = i % NDB;
+      return ld_tr<D>(sV[stv], to, kl / 16 + j, db);
+    };
+    // Block g needs element masks when it crosses seq_lens_k or the diagonal of
+    // this wave's first query.
+    auto needs_mask = [&](int g) SIGATTN_INLINE {
+      return (32 * g + 32 > Lk) || (CAUSAL && 32 * g + 31 > qw);
+    };
+    // Zeroes the P entries of block g whose key lies before 0 (pipeline fill),
+    // at or past seq_lens_k, or after the lane's query.  Works on the packed
+    // words, so garbage scores of such keys never matter.
+    auto mask_words = [&](uint32_t (&pk)[NCB][8], int g) SIGATTN_INLINE {
+      int kbase = 32 * g;
+      asm volatile("" : "+s"(kbase));  // keeps this rare fix-up in its own branch
+  #pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const unsigned lim = CAUSAL ? (unsigned)min(Lk, myq0 + 32 * cb + 1) : (unsigned)Lk;
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 2 * e;
+          const unsigned k0 = (unsigned)(kbase + 8 * (i / 4) + 4 * hi + (i % 4));
+          const uint32_t m = (k0 < lim ? 0x0000ffffu : 0u) | (k0 + 1u < lim ? 0xffff0000u : 0u);
+          pk[cb][e] &= m;
         }
       }
-      // One wait for this step's operand.
-      asm volatile("" ::"v"(opq[step % LA]));
-      const u32x4 a = opq[step % LA];
-      if (step < NKS) {
-#pragma unroll
-        for (int c2 = 0; c2 < NCB; ++c2) sc[c2] = Elem<T>::mfma(a, qf[c2][step], step == 0 ? zero16() : sc[c2]);
-      } else {
-        const int i = step - NKS, j = i / NDB, db = i % NDB;
-#pragma unroll
-        for (int c2 = 0; c2 < NCB; ++c2) {
-          const u32x4 bp = (u32x4){pp[c2][4 * j], pp[c2][4 * j + 1], pp[c2][4 * j + 2], pp[c2][4 * j + 3]};
-          acc[c2][db] = Elem<T>::mfma(a, bp, acc[c2][db]);
-        }
-      }
-      if (step + LA < NSTEP) opq[step % LA] = read_op(step + LA, STC, STV, KL);
-      else opq[step % LA] = read_op(step + LA - NSTEP, STCn, STVn, KLn);
-      // Sigmoid words of this step: stage B (reciprocal, packing) of word wd
-      // from ea, then stage A (exp2) of the next word into ea -- in the last
-      // word, of block r's first word (its Sᵀ chains are complete by then).
-#pragma unroll
-      for (int wd = step * NWD / NSTEP; wd < (step + 1) * NWD / NSTEP; ++wd) {
-        {
-          const int cb = wd / 8, e = wd % 8;
-          const float a0 = __builtin_amdgcn_rcpf(1.0f + ea[0]);
-          const float a1 = __builtin_amdgcn_rcpf(1.0f + ea[1]);
-          pn[cb][e] = Elem<T>::pack(a0, a1);
-          asm volatile("" : "+v"(pn[cb][e]));
-        }
-        if (wd + 1 < NWD) {
-          const int cb = (wd + 1) / 8, e = (wd + 1) % 8;
-          ea[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[cb][2 * e], nsl, c[2 * e]));
-          ea[1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[cb][2 * e + 1], nsl, c[2 * e + 1]));
-        } else {
-          ea[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[0][0], nsl, cn[0]));
-          ea[1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[0][1], nsl, cn[1]));
-        }
-      }
-#pragma unroll
-      for (int c2 = 0; c2 < NCB; ++c2) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, 5 * NWD / NSTEP / NCB + 1, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (r == 0 || needs_mask(r - 1)) mask_words(pn, r - 1);
-  };
+    };
 
-  // Pipeline fill: Pᵀ(-2) = Pᵀ(-1) = 0 (the latter through its mask).  The
-  // Vᵀ operands of blocks -2 and -1 come from ring stage NST-1, zeroed here
-  // (tile NST-1 is copied into it from the barrier of region 2·NST-5 on,
-  // after every read of blocks -2 and -1), so 0 * operand stays 0.
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-#pragma unroll
-    for (int c2 = 0; c2 < NCB; ++c2) {
-      sbuf[x][c2] = zero16();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pbuf[x][c2][e] = 0u;
-    }
-  }
-  ea[0] = ea[1] = 0.0f;
-  for (int i = tid; i < BN * D / 8; i += 64 * NWV) *(u32x4 *)&sV[NST - 1][8 * i] = zero4();
+    f32x16 sbuf[2][NCB];        // Sᵀ accumulators, by block parity
+    uint32_t pbuf[2][NCB][8];   // packed P words, by block parity
+    u32x4 opq[LA];              // A operands of the next LA steps (slot = step % LA)
+    float ea[2];                // exp2 terms of the next word (sigmoid stage A)
 
-  if (ntiles > 0) {
-    issue(0, 0);
-    wait_dma();
-    if (SCOREMOD && tid < BN) sC[tid] = creg;
-  }
-  __syncthreads();
-  if (ntiles > 1) issue(1, 1);
-#pragma unroll
-  for (int o = 0; o < LA; ++o) opq[o] = read_op(o, 0, NST - 1, 0);
-
-  // This wave computes only up to its own last visible key block (causal) and
-  // not at all past seq_lens_q; afterwards it only takes part in the tile
-  // barriers and copies, leaving its SIMD to the other wave there.
-  int NBw = NB;
-  if (CAUSAL) NBw = min(NBw, (qw + QW - 1) / 32 + 1);
-  if (qw >= Lq) NBw = 0;
-  const int RW = NBw > 0 ? NBw + 2 : 0;
-  // One pass of the loop covers 2·NST regions (NST tiles), so region r0 + U
-  // starts tile r0/2 + U/2 with r0/2 a multiple of NST: every stage index in
-  // region() is a compile-time function of U.
-  for (int r0 = 0; r0 < RW; r0 += 2 * NST) {
-    Unroll<0, 2 * NST>::run([&](auto u) SIGATTN_INLINE {
-      if (r0 + decltype(u)::value < RW) region(r0 + decltype(u)::value, u);
-    });
-  }
-  // The rest of the workgroup's regions: the same barriers and copies.
-  for (int r = RW | 1; r < NB + 2; r += 2) {
-    const int u = (r + 1) / 2;
-    if (u < ntiles) {
-      wait_dma();
-      if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
-      if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if (u + 1 < ntiles) issue((u + 1) % NST, u + 1);
-    }
-  }
-
-  // Oᵀ accumulators -> O rows (4 consecutive d per 8-byte store).
-#pragma unroll
-  for (int c = 0; c < NCB; ++c) {
-    const int q = myq0 + 32 * c;
-    if (q < p.q_rows_out(Lq)) {
-      uint16_t *orow = Ob + (int64_t)q * p.sq_t;
-      const bool valid = q < Lq;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
+    // Region r (U = r mod 8, so every slot and ring stage is static):
+    //   MFMA: Sᵀ(r) = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ(r-2), one step = NCB MFMAs (one per
+    //         column block) sharing an A operand read LA steps earlier;
+    //   VALU: P(r-1) = sigmoid(Sᵀ(r-1)) as a two-stage pipeline over packed
+    //         words (exp2 of the next word, then reciprocal and packing);
+    //   LDS:  the operand LA steps ahead (wrapping into region r+1).
+    // Block g lives in tile g/2 (rows 32*(g%2)) in ring stage (g/2)%4.  In odd
+    // regions r = 2u-1, step BAR publishes tile u (its first read, the K rows of
+    // block r+1, comes next) and starts the copy of tile u+1 into the stage of
+    // tile u+1-NST.  With four stages that tile's last reads were issued two
+    // regions earlier, so the barrier needs no wait for this wave's own LDS
+    // reads; with three (D = 64) they were issued in this region, and every
+    // wave waits for them before the barrier.
+    auto region = [&](int r, auto u_tag) SIGATTN_INLINE {
+      constexpr int U = decltype(u_tag)::value;
+      constexpr int SL = U % 2;                    // parity of blocks r and r-2
+      constexpr int KL = 32 * (U % 2), KLn = 32 * ((U + 1) % 2);
+      constexpr int STC = (U / 2) % NST;           // stage of block r
+      constexpr int STV = ((U + 2 * NST - 2) / 2) % NST;  // stage of block r-2
+      constexpr int STCn = ((U + 1) / 2) % NST;    // stage of block r+1
+      constexpr int STVn = ((U + 2 * NST - 1) / 2) % NST;  // stage of block r-1
+      f32x16(&sc)[NCB] = sbuf[SL];
+      const f32x16(&sp)[NCB] = sbuf[1 - SL];
+      uint32_t(&pn)[NCB][8] = pbuf[1 - SL];
+      const uint32_t(&pp)[NCB][8] = pbuf[SL];
+      float c[16];   // exp2 offsets of block r-1 (per key row)
+      float cn[2];   // ... of block r's first word
+      if constexpr (SCOREMOD) {
+  #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          u32x2 o;
-          o.x = Elem<T>::pack(acc[c][db][4 * g + 0], acc[c][db][4 * g + 1]);
-          o.y = Elem<T>::pack(acc[c][db][4 * g + 2], acc[c][db][4 * g + 3]);
-          if (!valid) o = (u32x2){0u, 0u};
-          *(u32x2 *)(orow + d0) = o;
+          const float4 cv = *(const float4 *)&sC[STVn * BN + KLn + 8 * g + 4 * hi];
+          c[4 * g + 0] = cv.x; c[4 * g + 1] = cv.y; c[4 * g + 2] = cv.z; c[4 * g + 3] = cv.w;
+        }
+  #pragma unroll
+        for (int i = 0; i < 2; ++i) cn[i] = sC[STC * BN + KL + 4 * hi + i];
+      } else {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = nbl;
+        cn[0] = cn[1] = nbl;
+      }
+  #pragma unroll
+      for (int step = 0; step < NSTEP; ++step) {
+        if ((U % 2) == 1 && step == BAR) {
+          const int u = (r + 1) / 2;
+          if (u < ntiles) {
+            wait_dma();
+            if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
+            // With three stages the copy below refills the stage this region's
+            // Vᵀ operands came from: every wave's reads of it complete first.
+            if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (u + 1 < ntiles) issue((u + 1) % NST, u + 1);
+          }
+        }
+        // One wait for this step's operand.
+        asm volatile("" ::"v"(opq[step % LA]));
+        const u32x4 a = opq[step % LA];
+        if (step < NKS) {
+  #pragma unroll
+          for (int c2 = 0; c2 < NCB; ++c2) sc[c2] = Elem<T>::mfma(a, qf[c2][step], step == 0 ? zero16() : sc[c2]);
+        } else {
+          const int i = step - NKS, j = i / NDB, db = i % NDB;
+  #pragma unroll
+          for (int c2 = 0; c2 < NCB; ++c2) {
+            const u32x4 bp = (u32x4){pp[c2][4 * j], pp[c2][4 * j + 1], pp[c2][4 * j + 2], pp[c2][4 * j + 3]};
+            acc[c2][db] = Elem<T>::mfma(a, bp, acc[c2][db]);
+          }
+        }
+        if (step + LA < NSTEP) opq[step % LA] = read_op(step + LA, STC, STV, KL);
+        else opq[step % LA] = read_op(step + LA - NSTEP, STCn, STVn, KLn);
+        // Sigmoid words of this step: stage B (reciprocal, packing) of word wd
+        // from ea, then stage A (exp2) of the next word into ea -- in the last
+        // word, of block r's first word (its Sᵀ chains are complete by then).
+  #pragma unroll
+        for (int wd = step * NWD / NSTEP; wd < (step + 1) * NWD / NSTEP; ++wd) {
+          {
+            const int cb = wd / 8, e = wd % 8;
+            const float a0 = __builtin_amdgcn_rcpf(1.0f + ea[0]);
+            const float a1 = __builtin_amdgcn_rcpf(1.0f + ea[1]);
+            pn[cb][e] = Elem<T>::pack(a0, a1);
+            asm volatile("" : "+v"(pn[cb][e]));
+          }
+          if (wd + 1 < NWD) {
+            const int cb = (wd + 1) / 8, e = (wd + 1) % 8;
+            ea[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[cb][2 * e], nsl, c[2 * e]));
+            ea[1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[cb][2 * e + 1], nsl, c[2 * e + 1]));
+          } else {
+            ea[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[0][0], nsl, cn[0]));
+            ea[1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[0][1], nsl, cn[1]));
+          }
+        }
+  #pragma unroll
+        for (int c2 = 0; c2 < NCB; ++c2) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 5 * NWD / NSTEP / NCB + 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (r == 0 || needs_mask(r - 1)) mask_words(pn, r - 1);
+    };
+
+    // Pipeline fill: Pᵀ(-2) = Pᵀ(-1) = 0 (the latter through its mask).  The
+    // Vᵀ operands of blocks -2 and -1 come from ring stage NST-1, zeroed here
+    // (tile NST-1 is copied into it from the barrier of region 2·NST-5 on,
+    // after every read of blocks -2 and -1), so 0 * operand stays 0.
+  #pragma unroll
+    for (int x = 0; x < 2; ++x) {
+  #pragma unroll
+      for (int c2 = 0; c2 < NCB; ++c2) {
+        sbuf[x][c2] = zero16();
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) pbuf[x][c2][e] = 0u;
+      }
+    }
+    ea[0] = ea[1] = 0.0f;
+    for (int i = tid; i < BN * D / 8; i += 64 * NWV) *(u32x4 *)&sV[NST - 1][8 * i] = zero4();
+
+    if (ntiles > 0) {
+      issue(0, 0);
+      wait_dma();
+      if (SCOREMOD && tid < BN) sC[tid] = creg;
+    }
+    __syncthreads();
+    if (ntiles > 1) issue(1, 1);
+  #pragma unroll
+    for (int o = 0; o < LA; ++o) opq[o] = read_op(o, 0, NST - 1, 0);
+
+    // This wave computes only up to its own last visible key block (causal) and
+    // not at all past seq_lens_q; afterwards it only takes part in the tile
+    // barriers and copies, leaving its SIMD to the other wave there.
+    int NBw = NB;
+    if (CAUSAL) NBw = min(NBw, (qw + QW - 1) / 32 + 1);
+    if (qw >= Lq) NBw = 0;
+    const int RW = NBw > 0 ? NBw + 2 : 0;
+    // One pass of the loop covers 2·NST regions (NST tiles), so region r0 + U
+    // starts tile r0/2 + U/2 with r0/2 a multiple of NST: every stage index in
+    // region() is a compile-time function of U.
+    for (int r0 = 0; r0 < RW; r0 += 2 * NST) {
+      Unroll<0, 2 * NST>::run([&](auto u) SIGATTN_INLINE {
+        if (r0 + decltype(u)::value < RW) region(r0 + decltype(u)::value, u);
+      });
+    }
+    // The rest of the workgroup's regions: the same barriers and copies.
+    for (int r = RW | 1; r < NB + 2; r += 2) {
+      const int u = (r + 1) / 2;
+      if (u < ntiles) {
+        wait_dma();
+        if (SCOREMOD && tid < BN) sC[(u % NST) * BN + tid] = creg;
+        if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (u + 1 < ntiles) issue((u + 1) % NST, u + 1);
+      }
+    }
+
+    // Oᵀ accumulators -> O rows (4 consecutive d per 8-byte store).
+  #pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+      const int q = myq0 + 32 * c;
+      if (q < p.q_rows_out(Lq)) {
+        uint16_t *orow = Ob + (int64_t)q * p.sq_t;
+        const bool valid = q < Lq;
+  #pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+  #pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d0 = db * 32 + 8 * g + 4 * hi;
+            u32x2 o;
+            o.x = Elem<T>::pack(acc[c][db][4 * g + 0], acc[c][db][4 * g + 1]);
+            o.y = Elem<T>::pack(acc[c][db][4 * g + 2], acc[c][db][4 * g + 3]);
+            if (!valid) o = (u32x2){0u, 0u};
+            *(u32x2 *)(orow + d0) = o;
+          }
         }
       }
     }
@@ -393,7 +421,10 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
   constexpr int NCB = SIGATTN_FWD_NCB, BM = NWV * 32 * NCB;
   KParams p = kp;
   p.nblk = (p.Tq + BM - 1) / BM;
-  const dim3 grid((unsigned)(p.nblk * p.B * p.H));
+  // Dense causal problems (the kernel's order when not ragged with B <= 64):
+  // two query blocks per workgroup.
+  const bool pairs = causal && kFwdCausalPairs && !(p.ragged() && p.B <= 64);
+  const dim3 grid((unsigned)((pairs ? (p.nblk + 1) / 2 : p.nblk) * p.B * p.H));
   const dim3 block(64 * NWV);
   if (causal) {
     if (scoremod) fwd_mfma_kernel<T, D, NWV, NCB, true, true><<<grid, block, 0, st>>>(p);
