@@ -142,6 +142,7 @@ struct KParams {
 // multiple of 8 and batch_base 16-byte aligned (MFMA-path requirements).
 __device__ __forceinline__ void zero_row_span(void *batch_base, int64_t row_elems, int row0, int row1,
                                               int part, int nparts, int tid, int nthreads) {
+  if (row1 <= row0) return;
   const int64_t n = (int64_t)(row1 - row0) * row_elems / 8;  // 16-byte pieces
   const int64_t c0 = n * part / nparts, c1 = n * (part + 1) / nparts;
   u32x4 *dst = (u32x4 *)((uint16_t *)batch_base + (int64_t)row0 * row_elems);
