@@ -225,3 +225,46 @@ def test_padded_forward_deterministic():
     a = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
     b = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_major_layout_equals_contiguous(D, causal):
+    """Tensors whose rows do not hold every head back to back (a head-major
+    [B, H, T, D] buffer viewed as [B, T, H, D]) go through the C ABI with
+    their own strides: padding row blocks then take the per-head zero-row
+    path instead of the contiguous span.  Every output and gradient equals
+    the contiguous layout's (public API) bit for bit, padding rows zero."""
+    import ctypes
+
+    from triton_sigmoid import _capi
+
+    B, T, H, dtype = 3, 520, 2, torch.bfloat16
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=60 + D, noise=False)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = ts.sigmoid_attention_padded(*leaves, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal)
+    o.backward(do)
+    want = [o.detach()] + [t.grad for t in leaves]
+
+    def head_major(t):  # same values, strides (H*T*D, D, T*D, 1)
+        return t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+
+    hq, hk, hv, hdo = (head_major(t) for t in (q, k, v, do))
+    assert hq.stride(1) == D and hq.stride(2) == T * D
+    outs = [head_major(torch.full_like(t, float("nan"))) for t in (q, q, k, k)]  # O, dQ, dK, dV
+    bias = -torch.log(sk.float())
+    scale = torch.full((), 1 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    lib = _capi.load_library()
+    pr = _capi._problem(hq, hk, hv, bias, None, scale, sq, sk, causal)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.sigattn_fwd_ws(ctypes.byref(pr), outs[0].data_ptr(), None, 0, stream) == 0
+    nbytes = _capi.bwd_workspace_bytes(lib, pr, hq.device)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=DEV)
+    rc = lib.sigattn_bwd_ws(ctypes.byref(pr), hdo.data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
+                            outs[3].data_ptr(), ws.data_ptr() if nbytes else None, nbytes, stream)
+    assert rc == 0, _capi.strerror(rc)
+    torch.cuda.synchronize()
+    for name, got, ref, lens in zip(("O", "dQ", "dK", "dV"), outs, want, (sq, sq, sk, sk)):
+        assert torch.equal(got, ref), f"{name} differs from the contiguous layout"
+        for b in range(B):
+            assert torch.all(got[b, int(lens[b]):] == 0), f"{name}: padding rows of batch {b} not zero"
