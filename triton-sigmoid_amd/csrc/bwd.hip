@@ -1222,16 +1222,29 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
   });
 }
 
+// Waves and ring stages of the D = 128 dQ-from-dS kernel.  Measured at
+// B=4 L=4096 H=16 D=128 (causal / non-causal, one run): 8 waves with 4 stages
+// (160 KB) 0.254 / 0.414 ms, with 3 stages 0.256 / 0.424 ms, with 2 stages
+// 0.284 / 0.478 ms; 4 waves (two workgroups per CU) with 3 or 4 stages
+// 0.265 / 0.44-0.45 ms.
+#ifndef SIGATTN_DQDS_NW_128
+#define SIGATTN_DQDS_NW_128 8
+#endif
+#ifndef SIGATTN_DQDS_NST_128
+#define SIGATTN_DQDS_NST_128 4
+#endif
+
 template <typename T, int D>
 static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
-  launch_rows<(D == 128 ? 512 : 256)>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+  constexpr int NW128 = SIGATTN_DQDS_NW_128, NST128 = SIGATTN_DQDS_NST_128;
+  launch_rows<(D == 128 ? 64 * NW128 : 256)>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
     // D = 128: 8 waves (512 query rows: each K row read serves twice the dS
     // of a 4-wave workgroup; two waves per SIMD), one 32-key block per stage
-    // in a 3-stage ring.  D = 64: 4 waves (the K rows of a 32-key stage do not
+    // in a 4-stage ring.  D = 64: 4 waves (the K rows of a 32-key stage do not
     // divide over 8 waves' copies), 6-stage ring.
     if constexpr (D == 128) {
-      if (causal) bwd_dq_ds_kernel<T, D, true, 8, 1, 3><<<grid, 512, 0, st>>>(p);
-      else bwd_dq_ds_kernel<T, D, false, 8, 1, 3><<<grid, 512, 0, st>>>(p);
+      if (causal) bwd_dq_ds_kernel<T, D, true, NW128, 1, NST128><<<grid, 64 * NW128, 0, st>>>(p);
+      else bwd_dq_ds_kernel<T, D, false, NW128, 1, NST128><<<grid, 64 * NW128, 0, st>>>(p);
     } else {
       if (causal) bwd_dq_ds_kernel<T, D, true, 4, 1, 6><<<grid, 256, 0, st>>>(p);
       else bwd_dq_ds_kernel<T, D, false, 4, 1, 6><<<grid, 256, 0, st>>>(p);
