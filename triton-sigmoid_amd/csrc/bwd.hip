@@ -987,6 +987,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
 // Per 32 keys a wave reads 4 KB of dS and runs 16 MFMAs: the kernel is bound
 // by HBM bandwidth.
 // ---------------------------------------------------------------------------
+#ifndef SIGATTN_DQDS_NT
+#define SIGATTN_DQDS_NT 1
+#endif
+constexpr bool kDqDsNT = SIGATTN_DQDS_NT != 0;
+
 template <typename T, int D, bool CAUSAL, int NW, int KB, int NST>
 __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) {
   constexpr int BM = 64 * NW, BN = 32 * KB;
@@ -1098,10 +1103,18 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) 
         for (int i = 0; i < 2; ++i) {
           uint16_t *dst = ds_slot(st, cb, kl) + 512 * i;
           const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-          asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                       :
-                       : "v"(soff[i]), "s"(src), "{m0}"(m0)
-                       : "memory");
+          // dS is read once: non-temporal loads keep it from displacing the
+          // K rows the other workgroups of this (batch, head) re-read.
+          if constexpr (kDqDsNT)
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                         :
+                         : "v"(soff[i]), "s"(src), "{m0}"(m0)
+                         : "memory");
+          else
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                         :
+                         : "v"(soff[i]), "s"(src), "{m0}"(m0)
+                         : "memory");
         }
       }
     }
