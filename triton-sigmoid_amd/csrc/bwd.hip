@@ -592,6 +592,16 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
 // which B reads in the next region (the two P buffers alternate by block
 // parity).
 // ---------------------------------------------------------------------------
+// Dense causal grids in dense_item's XCD-grouped order too: paired key
+// blocks make every workgroup's work equal, so grouping costs no balance, and
+// each XCD then reads the Q and dO rows of two (batch, head) pairs at a time
+// instead of eight.  Measured at B=4 L=4096 H=16 D=128 causal: HBM fetch
+// 757 -> 278 MB per launch (the algorithmic 268 MB), 0.661 -> 0.647 ms.
+#ifndef SIGATTN_DKDV_GROUPED
+#define SIGATTN_DKDV_GROUPED 1
+#endif
+constexpr bool kDkdvGrouped = SIGATTN_DKDV_GROUPED != 0;
+
 template <typename T, bool CAUSAL, bool SCOREMOD, bool DSOUT>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) {
   constexpr int D = 128;
@@ -629,7 +639,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   } else {
     const int BH = p.B * p.H;
     int bh;
-    dense_item(blockIdx.x, BH, (int)(gridDim.x / BH), !CAUSAL, bh, kblk0);
+    dense_item(blockIdx.x, BH, (int)(gridDim.x / BH), !CAUSAL || kDkdvGrouped, bh, kblk0);
     nitems = p.nblk - 1 - kblk0 > kblk0 ? 2 : 1;
     b = bh / p.H, h = bh % p.H;
   }

@@ -251,7 +251,9 @@ struct WorkOrder {
 //     XCD starts the row-block levels in the order the caller maps them to
 //     (heaviest first); grouping pairs there broke that order and made the
 //     causal kernels slower (measured at B=4 L=4096 H=16 D=128: dQ from dS
-//     0.254 -> 0.322 ms, forward 0.30 -> 0.33 ms).
+//     0.254 -> 0.322 ms, forward 0.30 -> 0.33 ms).  Causal kernels whose
+//     workgroups each run a pair of row blocks with equal total work (the
+//     D = 128 dK/dV kernel) use the grouped order.
 // B*H not a multiple of 8 keeps the plain order.
 __device__ __forceinline__ void dense_item(int id, int BH, int nper, bool grouped, int &bh, int &blk) {
   if (!grouped || BH % 8 != 0) {
