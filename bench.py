@@ -607,7 +607,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(every (batch, head) pair is independent; sharding is described in DESIGN.md). "
+              "(every (batch, head) pair is independent, so the work would shard across GPUs by heads). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
