@@ -119,6 +119,17 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
  * sigattn_fwd) runs the same kernel with one chunk per (batch, head), so no
  * workspace is touched.  The sum of fp32 partials is deterministic (fixed
  * chunks, fixed order) and matches sigattn_fwd within fp32 summation order.
+ *
+ * Range split of small dense grids (no counterpart in the reference): a
+ * dense non-causal problem taking the MFMA kernels whose workgroups (one per
+ * 128 or 256 queries of every (batch, head)) would leave at least half of
+ * the GPU's compute units idle, and whose keys number at least 1024, runs
+ * each query block's keys as 2-4 chunks of at least 512 keys in as many
+ * workgroups, whose fp32 partials the last one to finish adds in chunk
+ * order inside the same launch; sigattn_fwd_workspace_bytes then returns the
+ * partials' size (it asks the current device for its compute-unit count, and
+ * returns 0 without a device).  Deterministic, and equal to sigattn_fwd
+ * within fp32 summation order.
  */
 size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p);
 int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
@@ -147,6 +158,23 @@ int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream);
  */
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
                 void *dv, void *stream);
+
+/*
+ * The recompute backward with the range split of small dense grids (no
+ * counterpart in the reference): for a dense non-causal problem at head_dim
+ * 64 taking the MFMA kernels, whose dQ or dK/dV grid would leave at least
+ * half of the GPU's compute units idle, the dQ kernel runs each query
+ * block's keys and the dK/dV kernel each key block's queries as 2-4 chunks
+ * of at least 512 rows (so T >= 1024), the fp32
+ * partials added in chunk order by the last chunk to finish, inside the
+ * same launch.  sigattn_bwd_split_workspace_bytes(p) is the workspace it
+ * needs (0 when nothing splits, or without a device); with workspace NULL
+ * or when nothing splits, sigattn_bwd_split runs sigattn_bwd.  Results are
+ * deterministic and equal sigattn_bwd's within fp32 summation order.
+ */
+size_t sigattn_bwd_split_workspace_bytes(const sigattn_problem *p);
+int sigattn_bwd_split(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                      void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * The two halves of sigattn_bwd, one kernel each (the reference launches the

@@ -66,6 +66,13 @@ void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record(
 void launch_fwd_generic(const KParams &p, int, int, bool, hipStream_t) { record("fwd_generic", p); }
 void launch_bwd_dq_generic(const KParams &p, int, int, bool, hipStream_t) { record("dq_generic", p); }
 void launch_bwd_dkdv_generic(const KParams &p, int, int, bool, hipStream_t) { record("dkdv_generic", p); }
+int fwd_rows_per_workgroup(int D) { return (D == 64 ? 4 : 8) * 32; }
+int fwd_workgroups_per_cu(int D) { return D == 64 ? 3 : 1; }
+int bwd_dq_rows_per_workgroup() { return 128; }
+int bwd_dkdv_rows_per_workgroup() { return 128; }
+int bwd_dq_workgroups_per_cu(int D) { return D == 64 ? 3 : 2; }
+int bwd_dkdv_workgroups_per_cu(int D) { return D == 64 ? 2 : 1; }
+void launch_rs_clear(int *, int, hipStream_t) { g_calls.emplace_back("rs_clear"); }
 // The fixed scratch of sigattn_fwd_noalloc: any aligned address stands in.
 hipError_t splitkv_scratch(float **ptr) {
   *ptr = reinterpret_cast<float *>(uintptr_t(3) << 20);
@@ -75,6 +82,16 @@ hipError_t splitkv_scratch(float **ptr) {
 
 // The library maps hipGetLastError() after its launches; no launch happens here.
 extern "C" hipError_t hipGetLastError(void) { return hipSuccess; }
+// The device the range split sizes itself for: none until g_cus is set.
+static int g_cus = 0;
+extern "C" hipError_t hipGetDevice(int *dev) {
+  *dev = 0;
+  return g_cus > 0 ? hipSuccess : hipErrorNoDevice;
+}
+extern "C" hipError_t hipDeviceGetAttribute(int *value, hipDeviceAttribute_t, int) {
+  *value = g_cus;
+  return hipSuccess;
+}
 
 int main() {
   // --- validation: the error codes of tests/test_capi_cpu.py, for every entry point
@@ -204,6 +221,51 @@ int main() {
     p = base(2, 0, 2, 64);
     EXPECT(sigattn_fwd(&p, nullptr, nullptr) == 0 && sigattn_bwd(&p, nullptr, nullptr, nullptr, nullptr, nullptr) == 0);
     EXPECT(g_calls.empty());
+  }
+  {
+    // Range split of small dense non-causal grids, on a device of 256 CUs:
+    // B=2 L=1024 H=8 D=64 has 128 workgroups per kernel.
+    g_cus = 256;
+    sigattn_problem p = base(2, 1024, 8, 64);
+    // 128 items of 1024 keys: two chunks of 512 keys, one workgroup per CU.
+    const size_t fw = sigattn_fwd_workspace_bytes(&p);
+    EXPECT(fw == 512 + size_t(128) * 2 * 128 * 64 * 4);  // counters, then 2 partials per item
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw, nullptr) == 0 && calls() == "rs_clear,fwd_mfma");
+    EXPECT(g_last.rsplit == 2 && g_last.rs_cnt == kFake && (char *)g_last.rs_part == (char *)kFake + 512);
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw - 1, nullptr) == SIGATTN_ERR_WORKSPACE && g_calls.empty());
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_last.rsplit == 0);
+    EXPECT(sigattn_fwd_noalloc(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_last.rsplit == 0);
+    const size_t bw = sigattn_bwd_split_workspace_bytes(&p);
+    const size_t dq_bytes = 512 + size_t(128) * 2 * 128 * 64 * 4;
+    EXPECT(bw == dq_bytes + 512 + size_t(128) * 2 * 2 * 128 * 64 * 4);
+    EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, kFake, bw, nullptr) == 0 &&
+           calls() == "rs_clear,rs_clear,dq_mfma,dkdv_mfma");
+    EXPECT(g_last.rsplit == 2 && (char *)g_last.rs_cnt == (char *)kFake + dq_bytes);
+    EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, kFake, bw - 1, nullptr) == SIGATTN_ERR_WORKSPACE);
+    EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, nullptr, 0, nullptr) == 0 &&
+           calls() == "dq_mfma,dkdv_mfma" && g_last.rsplit == 0);
+    // Causal, padded, D = 128 backward, or grids that fill the GPU: no split.
+    sigattn_problem c = p;
+    c.causal = 1;
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    c = p;
+    c.seq_lens_q = c.seq_lens_k = (const int32_t *)kFake;
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    c = base(2, 1024, 8, 128);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) > 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    c = base(4, 1024, 8, 64);  // 256 items: the GPU is already half full
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    c = base(2, 1000, 8, 64);  // keys too few for two chunks of 512
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    // Four chunks at 2048 keys per item of 64 items (one workgroup per CU),
+    // and at 4096 keys per item of 128 items (chunks of 1024: two per CU).
+    c = base(1, 2048, 4, 64);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 256 + size_t(64) * 4 * 128 * 64 * 4);
+    c = base(1, 4096, 4, 64);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 512 + size_t(128) * 4 * 128 * 64 * 4);
+    c = base(1, 2048, 8, 64);  // 128 items: two chunks
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 512 + size_t(128) * 2 * 128 * 64 * 4);
+    g_cus = 0;
   }
   if (g_fail == 0) std::printf("capi sanitizer driver: all checks passed\n");
   return g_fail == 0 ? 0 : 1;

@@ -42,7 +42,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? 2 * BN : 4];
 
   int b, h, qb;
-  if (p.ragged() && p.B <= 64) {
+  int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its keys
+  if (!CAUSAL && p.rsplit > 1) {
+    int bh;
+    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    dense_item(ritem, p.B * p.H, p.nblk, true, bh, qb);
+    b = bh / p.H, h = bh % p.H;
+  } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
@@ -56,7 +62,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     b = bh / p.H, h = bh % p.H;
   }
   const int Lq = p.len_q(b);
-  const int Lk = p.len_k(b);
+  // Keys of this workgroup: under the range split, its chunk of the item's
+  // key tiles, indexed from the chunk's first key.
+  int key0 = 0, Lk = p.len_k(b);
+  if (!CAUSAL && p.rsplit > 1) {
+    const int ntk = (Lk + BN - 1) / BN;
+    key0 = split_tile(rchunk, p.rsplit, ntk) * BN;
+    Lk = min(Lk, split_tile(rchunk + 1, p.rsplit, ntk) * BN) - key0;
+  }
   // Padding item: its zero rows as part of one contiguous span (see zero_row_span).
   if (qb * BM >= Lq && p.q_rows_contiguous(D)) {
     zero_row_span((uint16_t *)p.dq + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
@@ -69,7 +82,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   const int q0 = qb * BM, qw = q0 + w * 32, my_q = qw + l32;
 
   const int64_t qoff = p.q_base(b, h);
-  const int64_t koff = p.k_base(b, h);
+  const int64_t koff = p.k_base(b, h) + (int64_t)key0 * p.sk_t;
   const uint16_t *Qb = (const uint16_t *)p.q + qoff;
   const uint16_t *dOb = (const uint16_t *)p.dout + qoff;
   const uint16_t *Kb = (const uint16_t *)p.k + koff;
@@ -172,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   auto load_c = [&](int n0) SIGATTN_INLINE {
     if (SCOREMOD && tid < BN) {
       const int key = n0 + tid;
-      creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
+      creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key0 + key]) * kLog2e : 0.0f;
     }
   };
   auto issue = [&](int st, int n0) SIGATTN_INLINE {
@@ -202,6 +215,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     iteration(it, std::integral_constant<int, 0>{});
     if (it + 1 < ntiles) iteration(it + 1, std::integral_constant<int, 1>{});
   }
+
+  if (!CAUSAL && p.rsplit > 1 &&
+      !split_combine<NDB, 4>([&](int i) SIGATTN_INLINE -> f32x16 & { return acc[i]; },
+                             p.rs_part + (int64_t)ritem * p.rsplit * (BM * D), p.rs_cnt + ritem, rchunk,
+                             p.rsplit, w, lane))
+    return;
 
   if (my_q < p.q_rows_out(Lq)) {
     uint16_t *row = dQb + (int64_t)my_q * p.sq_t;
@@ -256,7 +275,13 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   __shared__ __attribute__((aligned(16))) uint16_t sO[NST][BMQ * D];
 
   int b, h, kblk;
-  if (p.ragged() && p.B <= 64) {
+  int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its queries
+  if (!CAUSAL && !DSOUT && p.rsplit > 1) {
+    int bh;
+    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    dense_item(ritem, p.B * p.H, p.nblk, true, bh, kblk);
+    b = bh / p.H, h = bh % p.H;
+  } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lk, BN, p.nblk, false)
@@ -293,8 +318,14 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   uint16_t *dVb = (uint16_t *)p.dv + koff;
 
   // Causal: queries before the workgroup's first key see none of its keys.
-  const int mstart = CAUSAL ? (k0 / BMQ) * BMQ : 0;
-  const int mend = (k0 >= Lk) ? mstart : Lq;
+  // Range split: this workgroup's chunk of the item's query tiles.
+  int mstart = CAUSAL ? (k0 / BMQ) * BMQ : 0;
+  int mend = (k0 >= Lk) ? mstart : Lq;
+  if (!CAUSAL && !DSOUT && p.rsplit > 1 && k0 < Lk) {
+    const int ntq = (Lq + BMQ - 1) / BMQ;
+    mstart = split_tile(rchunk, p.rsplit, ntq) * BMQ;
+    mend = min(Lq, split_tile(rchunk + 1, p.rsplit, ntq) * BMQ);
+  }
   const int ntiles = mend > mstart ? (mend - mstart + BMQ - 1) / BMQ : 0;
   const int NB = 2 * ntiles;
 
@@ -542,6 +573,12 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     if (r0 + 6 < NB + 2) region(r0 + 6, std::integral_constant<int, 6>{});
     if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
   }
+
+  if (!CAUSAL && !DSOUT && p.rsplit > 1 &&
+      !split_combine<2 * NDB, 4>(
+          [&](int i) SIGATTN_INLINE -> f32x16 & { return i < NDB ? dka[i] : dva[i - NDB]; },
+          p.rs_part + (int64_t)ritem * p.rsplit * (2 * BN * D), p.rs_cnt + ritem, rchunk, p.rsplit, w, lane))
+    return;
 
   if (my_k < p.k_rows_out(Lk)) {
     uint16_t *kr = dKb + (int64_t)my_k * p.sk_t;
@@ -1210,6 +1247,8 @@ static void launch_rows(const KParams &kp, int rows, Launch &&launch) {
 template <typename T, int D>
 static void bwd_dq_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   launch_rows<128>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+    // Range split (dense non-causal): rsplit workgroups per item.
+    if (!causal && p.rsplit > 1) grid.x *= (unsigned)p.rsplit;
     if (causal) {
       if (sm) bwd_dq_kernel<T, D, true, true><<<grid, 256, 0, st>>>(p);
       else bwd_dq_kernel<T, D, true, false><<<grid, 256, 0, st>>>(p);
@@ -1235,6 +1274,8 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
       }
       return;
     }
+    // Range split (dense non-causal recompute backward): rsplit workgroups per item.
+    if (!causal && !DSOUT && p.rsplit > 1) grid.x *= (unsigned)p.rsplit;
     if (causal) {
       if (sm) bwd_dkdv_kernel<T, D, true, true, DSOUT><<<grid, 256, 0, st>>>(p);
       else bwd_dkdv_kernel<T, D, true, false, DSOUT><<<grid, 256, 0, st>>>(p);
@@ -1286,6 +1327,13 @@ static void by_type(int dtype, int D, F &&f) {
     else f((_Float16 *)nullptr, std::integral_constant<int, 64>{});
   }
 }
+
+int bwd_dq_rows_per_workgroup() { return 128; }
+int bwd_dkdv_rows_per_workgroup() { return 128; }
+// Resident workgroups per CU of the recompute kernels at D = 64 (dQ: 32 KB of
+// LDS and at most 168 VGPRs; dK/dV: 64 KB and 128 + 128 registers).
+int bwd_dq_workgroups_per_cu(int D) { return D == 64 ? 3 : 2; }
+int bwd_dkdv_workgroups_per_cu(int D) { return D == 64 ? 2 : 1; }
 
 void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool sm, hipStream_t st) {
   by_type(dtype, D, [&](auto *t, auto d) {

@@ -7,6 +7,7 @@
 // allocates or synchronises.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstdint>
 
@@ -100,6 +101,110 @@ SplitPlan splitkv_plan(const sigattn_problem *p, bool mfma) {
 
 int64_t splitkv_workspace_bytes(const sigattn_problem *p, const SplitPlan &sp) {
   return sp.nsplit > 1 ? (int64_t)sp.nsplit * p->B * p->H * p->Tq * p->D * (int64_t)sizeof(float) : 0;
+}
+
+bool is_ragged(const sigattn_problem *p) {
+  return p->seq_lens_q != nullptr || p->seq_lens_k != nullptr || p->cu_seqlens_q != nullptr ||
+         p->cu_seqlens_k != nullptr;
+}
+
+// Compute units of the current device (cached per device; 0 if unknown, e.g.
+// without a GPU).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Fewest rows of the streamed range (keys for the forward and dQ kernels,
+// queries for dK/dV) that a range-split chunk takes; chunks of at least
+// twice as many may run two workgroups per CU.
+#ifndef SIGATTN_RS_MIN_ROWS
+#define SIGATTN_RS_MIN_ROWS 512
+#endif
+
+// Range split of a small dense non-causal grid (KParams::rsplit).  A kernel
+// whose `items` workgroups leave at least half of the GPU's CUs idle runs
+// each item as n chunks of its streamed range of `rows`: the most chunks,
+// up to kRangeSplitMax, that keep every chunk at least SIGATTN_RS_MIN_ROWS
+// long and the grid within one workgroup per CU (two when chunks are at
+// least twice that long, and never more than the kernel's `per_cu_max`
+// resident workgroups).  Measured on MI355X (256 CUs), D = 64 fp16
+// non-causal, GPU time per forward+backward: B=2 L=1024 H=8 62.6 -> 59.2 us
+// (n = 2; n = 4 took 72.9), B=1 L=2048 H=8 107.9 -> 82.1 us (n = 2; n = 4
+// took 90.5), B=1 L=4096 H=4 198.6 -> 134.2 us (n = 4), B=1 L=16384 H=1
+// 759 -> 395 us (n = 4); grids filling half the GPU or more measured slower
+// split (B=4 L=1024 H=8 65.8 -> 80.7 us at n = 2).  Each chunk's partial is
+// `part_floats` fp32 per item, and each item has an int counter: the
+// workspace holds the counters first (256-byte aligned), then the partials.
+struct RangeSplit {
+  int n = 1;
+  int64_t items = 0, part_floats = 0, cnt_bytes = 0, bytes = 0;
+};
+
+RangeSplit range_split(int64_t items, int64_t cus, int64_t per_cu_max, int64_t rows, int64_t part_floats) {
+  RangeSplit r;
+  if (items <= 0 || cus <= 0 || 2 * items > cus) return r;
+  int64_t n = sigattn::kRangeSplitMax;
+  for (; n >= 2; --n) {
+    if (rows < n * SIGATTN_RS_MIN_ROWS) continue;
+    int64_t per_cu = rows >= 2 * n * SIGATTN_RS_MIN_ROWS ? 2 : 1;
+    if (per_cu > per_cu_max) per_cu = per_cu_max;
+    if (n * items <= cus * per_cu) break;
+  }
+  if (n < 2) return r;
+  r.n = (int)n;
+  r.items = items;
+  r.part_floats = part_floats;
+  r.cnt_bytes = cdiv(items * (int64_t)sizeof(int), 256) * 256;
+  r.bytes = r.cnt_bytes + items * n * part_floats * (int64_t)sizeof(float);
+  return r;
+}
+
+bool splittable(const sigattn_problem *p, bool mfma) {
+  return mfma && p->causal == 0 && !is_ragged(p) && p->Tq > 0 && p->Tk > 0 && p->B * p->H > 0;
+}
+
+RangeSplit fwd_range_split(const sigattn_problem *p, bool mfma) {
+  if (!splittable(p, mfma)) return RangeSplit{};
+  const int D = (int)p->D, BM = sigattn::fwd_rows_per_workgroup(D);
+  return range_split(p->B * p->H * cdiv(p->Tq, BM), device_cus(), sigattn::fwd_workgroups_per_cu(D), p->Tk,
+                     (int64_t)BM * D);
+}
+
+// The recompute backward's split (D = 64, whose backward is the recompute
+// one): the dQ kernel splits keys, the dK/dV kernel queries.
+struct BwdSplit {
+  RangeSplit dq, kv;
+  int64_t bytes = 0;
+};
+
+BwdSplit bwd_range_split(const sigattn_problem *p, bool mfma) {
+  BwdSplit s;
+  if (!splittable(p, mfma) || p->D != 64) return s;
+  const int D = 64, cus = device_cus();
+  const int RQ = sigattn::bwd_dq_rows_per_workgroup(), RK = sigattn::bwd_dkdv_rows_per_workgroup();
+  s.dq = range_split(p->B * p->H * cdiv(p->Tq, RQ), cus, sigattn::bwd_dq_workgroups_per_cu(D), p->Tk,
+                     (int64_t)RQ * D);
+  s.kv = range_split(p->B * p->H * cdiv(p->Tk, RK), cus, sigattn::bwd_dkdv_workgroups_per_cu(D), p->Tq,
+                     2 * (int64_t)RK * D);
+  s.bytes = s.dq.bytes + s.kv.bytes;
+  return s;
+}
+
+// Sets k's range-split fields for `r` over the workspace at `ws` and clears
+// its counters on `st`.
+void use_range_split(KParams &k, const RangeSplit &r, void *ws, hipStream_t st) {
+  k.rsplit = r.n;
+  k.rs_cnt = (int *)ws;
+  k.rs_part = (float *)((char *)ws + r.cnt_bytes);
+  sigattn::launch_rs_clear(k.rs_cnt, (int)r.items, st);
 }
 
 // Two-pass backward: bytes of dS tiles (DsLayout) per head, over all batches.
@@ -196,14 +301,18 @@ size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p) {
   // Pointers are not known yet: assume aligned rows (a misaligned call later
   // takes the portable kernel and ignores the workspace).
   const void *none[1] = {nullptr};
-  return (size_t)splitkv_workspace_bytes(p, splitkv_plan(p, use_mfma(p, none, 0)));
+  const bool mfma = use_mfma(p, none, 0);
+  const SplitPlan sp = splitkv_plan(p, mfma);
+  if (sp.nsplit > 0) return (size_t)splitkv_workspace_bytes(p, sp);
+  return (size_t)fwd_range_split(p, mfma).bytes;
 }
 
 static_assert(sigattn::kSplitScratchBytes == SIGATTN_NOALLOC_SCRATCH_BYTES, "scratch size");
 
 // Forward: the split-KV partials go to `workspace` (caller memory), to the
 // library's fixed scratch array (static_scratch), or nowhere (one chunk per
-// (batch, head)).
+// (batch, head)).  The range split of small dense grids runs only with a
+// caller workspace.
 static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,
                     bool static_scratch, void *stream) {
   const int rc = sigattn_check(p);
@@ -229,7 +338,13 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     sp.nsplit = 1;  // no workspace: one chunk per (batch, head), written directly
     sp.chunk = (int)(cdiv(p->Tk, 128) * 128);
   }
+  RangeSplit rs;
+  if (sp.nsplit == 0 && workspace != nullptr && !static_scratch) {
+    rs = fwd_range_split(p, mfma);
+    if (rs.n > 1 && ((size_t)rs.bytes > workspace_bytes || !aligned16(workspace))) return SIGATTN_ERR_WORKSPACE;
+  }
   (void)hipGetLastError();
+  if (rs.n > 1) use_range_split(k, rs, workspace, st);
   if (sp.nsplit > 0) {
     k.nsplit = sp.nsplit;
     k.chunk = sp.chunk;
@@ -343,6 +458,38 @@ int sigattn_bwd_ws(const sigattn_problem *p, const void *dout, void *dq, void *d
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
                 void *stream) {
   return bwd_impl(p, dout, dq, dk, dv, nullptr, 0, stream, kBwdAll);
+}
+
+size_t sigattn_bwd_split_workspace_bytes(const sigattn_problem *p) {
+  if (sigattn_check(p) != SIGATTN_OK || p->B == 0 || p->H == 0) return 0;
+  const void *none[1] = {nullptr};
+  return (size_t)bwd_range_split(p, use_mfma(p, none, 0)).bytes;
+}
+
+int sigattn_bwd_split(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+  const int rc = sigattn_check(p);
+  if (rc != SIGATTN_OK) return rc;
+  if (p->B == 0 || p->H == 0) return SIGATTN_OK;
+  const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
+  const BwdSplit bs = workspace != nullptr ? bwd_range_split(p, use_mfma(p, ptrs, 7)) : BwdSplit{};
+  if (bs.bytes == 0) return bwd_impl(p, dout, dq, dk, dv, nullptr, 0, stream, kBwdAll);
+  if ((size_t)bs.bytes > workspace_bytes || !aligned16(workspace)) return SIGATTN_ERR_WORKSPACE;
+  if (dq == nullptr || dk == nullptr || dv == nullptr || dout == nullptr) return SIGATTN_ERR_NULL_ARG;
+  KParams k = make_params(p);
+  k.dout = dout;
+  k.dq = dq;
+  k.dk = dk;
+  k.dv = dv;
+  const hipStream_t st = (hipStream_t)stream;
+  const bool sm = p->score_mod != nullptr;
+  (void)hipGetLastError();
+  KParams kq = k, kk = k;
+  if (bs.dq.n > 1) use_range_split(kq, bs.dq, workspace, st);
+  if (bs.kv.n > 1) use_range_split(kk, bs.kv, (char *)workspace + bs.dq.bytes, st);
+  sigattn::launch_bwd_dq_mfma(kq, p->dtype, (int)p->D, false, sm, st);
+  sigattn::launch_bwd_dkdv_mfma(kk, p->dtype, (int)p->D, false, sm, false, st);
+  return launch_status();
 }
 
 int sigattn_bwd_dq(const sigattn_problem *p, const void *dout, void *dq, void *stream) {

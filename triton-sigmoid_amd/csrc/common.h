@@ -24,6 +24,7 @@ namespace sigattn {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -92,6 +93,14 @@ struct KParams {
   // written by the dK/dV kernel and read by the dQ-from-dS kernel.
   uint16_t *ds;
   int ds_nqb, ds_nkb;  // 32-row query / key blocks per (batch, head): ceil(Tq/32), ceil(Tk/32)
+  // Range split of small dense non-causal grids (rsplit <= 1: off): every
+  // work item's streamed range (keys for the forward and dQ kernels, queries
+  // for dK/dV) runs as rsplit chunks in rsplit workgroups, which hand their
+  // fp32 accumulators over through rs_part (rsplit partials per item) and
+  // count themselves in rs_cnt[item] (zero at launch); see split_combine.
+  int rsplit;
+  float *rs_part;
+  int *rs_cnt;
 
   // Valid query / key rows of batch b.
   __device__ __forceinline__ int len_q(int b) const {
@@ -560,6 +569,95 @@ constexpr int kBufferWord3 = 0x00020000;
 // the two-pass backward costs the dK/dV kernel 0.10 ms at the headline shape
 // with it, 0.16 ms without).
 constexpr int kStoreNT = 2;
+
+// Chunk c of n of a range of nt tiles: tiles [c*nt/n, (c+1)*nt/n).
+// (c < n <= 8 and nt < 2^26, so 32-bit arithmetic; wave-uniform, kept in an
+// SGPR for the tile copies' base addresses.)
+__device__ __forceinline__ int split_tile(int c, int n, int nt) {
+  return __builtin_amdgcn_readfirstlane(c * nt / n);
+}
+
+// Most chunks a range-split item runs as (KParams::rsplit).
+constexpr int kRangeSplitMax = 4;
+
+// End of a range-split work item (KParams::rsplit): the workgroup's fp32
+// accumulators -- NACC f32x16 per lane, acc(i) -- become the item's final
+// sum, or the workgroup learns that another chunk will write the output.
+// Every chunk stores its accumulators to its slot of the item's partials
+// (lane-major, 1 KB per store instruction) and, once the stores have
+// completed, counts itself in; the workgroup whose count completes the item
+// adds all n partials in chunk order, its own from registers, so the sum
+// does not depend on which chunk finishes last.  The partials move through
+// agent-coherent (sc1) buffer accesses around a relaxed agent-scope counter:
+// an agent-scope fence instead would write back and invalidate the whole L2
+// of the XCD, evicting the tiles other workgroups stream.  The other chunks'
+// partials are loaded two accumulators at a time with every chunk's loads in
+// flight together (one memory round trip per pair, not one per chunk).
+// Returns false when this workgroup should exit without writing.
+template <int NACC, int NW, class Acc>
+__device__ __forceinline__ bool split_combine(Acc &&acc, float *part_item, int *cnt, int chunk, int n, int w,
+                                              int lane) {
+  constexpr int kCoherent = 16;  // cache-policy operand of the buffer builtins: sc1
+  constexpr int kWaveBytes = NACC * 4 * 1024;
+  constexpr int G = NACC % 2 == 0 ? 2 : 1;  // accumulators per round trip
+  constexpr int kOthers = kRangeSplitMax - 1;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)part_item, (short)0, n * NW * kWaveBytes, kBufferWord3);
+  const int mine = (chunk * NW + w) * kWaveBytes + 16 * lane;
+#pragma unroll
+  for (int i = 0; i < NACC; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x16 &a = acc(i);
+      const f32x4 v = {a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, mine + (4 * i + g) * 1024, 0,
+                                             kCoherent);
+    }
+  __shared__ int arrived;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (arrived != n - 1) return false;
+  asm volatile("" ::: "memory");
+  // Slot j of `other` holds chunk j (j < chunk) or chunk j + 1 (j >= chunk).
+  int off[kOthers];
+#pragma unroll
+  for (int j = 0; j < kOthers; ++j) off[j] = ((j < chunk ? j : j + 1) * NW + w) * kWaveBytes + 16 * lane;
+#pragma unroll
+  for (int i0 = 0; i0 < NACC; i0 += G) {
+    f32x4 other[kOthers][G][4];
+#pragma unroll
+    for (int j = 0; j < kOthers; ++j)
+      if (j + 1 < n)  // wave-uniform: chunk count
+#pragma unroll
+        for (int ii = 0; ii < G; ++ii)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            // Whole-vector casts: hipcc 7.2 compiles a __builtin_bit_cast of
+            // a single ext_vector element as a read of element 0.
+            other[j][ii][g] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off[j] + (4 * (i0 + ii) + g) * 1024, 0, kCoherent));
+#pragma unroll
+    for (int ii = 0; ii < G; ++ii) {
+      f32x16 &a = acc(i0 + ii);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 own = {a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+        f32x4 sum = chunk == 0 ? own : other[0][ii][g];
+#pragma unroll
+        for (int c = 1; c < kRangeSplitMax; ++c) {
+          if (c >= n) break;
+          // Chunk c's partial: own (c == chunk), slot c (c < chunk) or slot c - 1.
+          const f32x4 below = other[c < kOthers ? c : kOthers - 1][ii][g];
+          sum += c == chunk ? own : (c < chunk ? below : other[c - 1][ii][g]);
+        }
+        a[4 * g] = sum.x, a[4 * g + 1] = sum.y, a[4 * g + 2] = sum.z, a[4 * g + 3] = sum.w;
+      }
+    }
+  }
+  return true;
+}
 
 // Per-lane element offsets into swizzled [*, D] tiles, computed once per
 // kernel.  A row offset that is a multiple of 16 rows leaves swz() unchanged,

@@ -87,7 +87,14 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? NST * BN : 4];
 
   int b, h, qb0, nitems = 1;
-  if (p.ragged() && p.B <= 64) {
+  int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its keys
+  if (!CAUSAL && p.rsplit > 1) {
+    // Small dense grids: the rsplit workgroups of an item take adjacent ids.
+    int bh;
+    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    dense_item(ritem, p.B * p.H, p.nblk, true, bh, qb0);
+    b = bh / p.H, h = bh % p.H;
+  } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true)
@@ -126,7 +133,14 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
     // The previous item's last LDS reads precede this item's tile fills.
     if (item > 0) __syncthreads();
     const int Lq = p.len_q(b);
-    const int Lk = p.len_k(b);
+    // Keys of this workgroup: under the range split, its chunk of the item's
+    // key tiles, indexed from the chunk's first key.
+    int key0 = 0, Lk = p.len_k(b);
+    if (!CAUSAL && p.rsplit > 1) {
+      const int ntk = (Lk + BN - 1) / BN;
+      key0 = split_tile(rchunk, p.rsplit, ntk) * BN;
+      Lk = min(Lk, split_tile(rchunk + 1, p.rsplit, ntk) * BN) - key0;
+    }
     // Padding item (the row block lies wholly past seq_lens_q): its zero rows
     // as part of one contiguous span over all heads when the layout allows.
     if (qb * BM >= Lq && nitems == 1 && p.q_rows_contiguous(D)) {
@@ -146,7 +160,7 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
     const int qw = q0 + slot * QW;    // this wave's first query
     const int myq0 = qw + l32;        // this lane's query in column block 0 (block c: +32c)
 
-    const int64_t qoff = p.q_base(b, h), koff = p.k_base(b, h);
+    const int64_t qoff = p.q_base(b, h), koff = p.k_base(b, h) + (int64_t)key0 * p.sk_t;
     const uint16_t *Qb = (const uint16_t *)p.q + qoff;
     const uint16_t *Kb = (const uint16_t *)p.k + koff;
     const uint16_t *Vb = (const uint16_t *)p.v + koff;
@@ -196,7 +210,7 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
     auto load_c = [&](int n0) SIGATTN_INLINE {
       if (SCOREMOD && tid < BN) {
         const int key = n0 + tid;
-        creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key]) * kLog2e : 0.0f;
+        creg = key < Lk ? -(bias + p.score_mod[p.mod_base(b) + key0 + key]) * kLog2e : 0.0f;
       }
     };
     auto issue = [&](int st, int t) SIGATTN_INLINE {
@@ -402,6 +416,12 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
       }
     }
 
+    if (!CAUSAL && p.rsplit > 1 &&
+        !split_combine<NCB * NDB, NWV>([&](int i) SIGATTN_INLINE -> f32x16 & { return acc[i / NDB][i % NDB]; },
+                                       p.rs_part + (int64_t)ritem * p.rsplit * (BM * D), p.rs_cnt + ritem,
+                                       rchunk, p.rsplit, w, lane))
+      return;
+
     // Oᵀ accumulators -> O rows (4 consecutive d per 8-byte store).
   #pragma unroll
     for (int c = 0; c < NCB; ++c) {
@@ -442,7 +462,8 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
   // Dense causal problems (the kernel's order when not ragged with B <= 64):
   // two query blocks per workgroup.
   const bool pairs = causal && kFwdCausalPairs && !(p.ragged() && p.B <= 64);
-  const dim3 grid((unsigned)((pairs ? (p.nblk + 1) / 2 : p.nblk) * p.B * p.H));
+  if (causal || p.rsplit < 1) p.rsplit = 1;
+  const dim3 grid((unsigned)((pairs ? (p.nblk + 1) / 2 : p.nblk) * p.B * p.H * p.rsplit));
   const dim3 block(64 * NWV);
   if (causal) {
     if (scoremod) fwd_mfma_kernel<T, D, NWV, NCB, true, true><<<grid, block, 0, st>>>(p);
@@ -462,6 +483,16 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
 template <typename T, int D>
 static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
   launch_fwd_w<T, D, (D == 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
+}
+
+int fwd_rows_per_workgroup(int D) { return (D == 64 ? 4 : 8) * 32; }
+int fwd_workgroups_per_cu(int D) { return D == 64 ? fwd_occupancy<64>() : fwd_occupancy<128>(); }
+
+__global__ __launch_bounds__(256) void rs_clear_kernel(int *cnt, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) cnt[i] = 0;
+}
+void launch_rs_clear(int *cnt, int n, hipStream_t st) {
+  if (n > 0) rs_clear_kernel<<<(unsigned)min((n + 255) / 256, 64), 256, 0, st>>>(cnt, n);
 }
 
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,

@@ -12,6 +12,19 @@ constexpr int kF16 = 0;
 constexpr int kBF16 = 1;
 constexpr int kF32 = 2;
 
+// Rows per workgroup and resident workgroups per CU of the MFMA forward and
+// of the recompute backward's kernels (D in {64, 128}); the range split of
+// small dense grids (KParams::rsplit) sizes itself from them.
+int fwd_rows_per_workgroup(int D);
+int fwd_workgroups_per_cu(int D);
+int bwd_dq_rows_per_workgroup();
+int bwd_dkdv_rows_per_workgroup();
+int bwd_dq_workgroups_per_cu(int D);
+int bwd_dkdv_workgroups_per_cu(int D);
+// Zeroes n range-split arrival counters on `st` (a kernel: no memset node
+// lands in a captured graph).
+void launch_rs_clear(int *cnt, int n, hipStream_t st);
+
 // MFMA kernels: dtype in {kF16, kBF16}, D in {64, 128}, 16-byte aligned rows.
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
                      hipStream_t st);

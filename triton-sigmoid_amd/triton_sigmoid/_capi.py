@@ -79,6 +79,9 @@ SIGNATURES = {
     "sigattn_bwd_dkdv_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_size_t,
                              _c_vp], _c_i32),
     "sigattn_bwd_dq_ws": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, ctypes.c_size_t, _c_vp], _c_i32),
+    "sigattn_bwd_split_workspace_bytes": ([ctypes.POINTER(SigattnProblem)], ctypes.c_size_t),
+    "sigattn_bwd_split": ([ctypes.POINTER(SigattnProblem), _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_size_t,
+                           _c_vp], _c_i32),
 }
 
 _lib = None
@@ -293,9 +296,16 @@ def _bwd_workspace(nbytes: int, device: torch.device):
 def _launch_bwd(lib, pr: SigattnProblem, dO, dQ, dK, dV) -> None:
     """sigattn_bwd_ws with a workspace from torch's caching allocator when
     the two-pass backward applies (bwd_workspace_bytes) and the allocation
-    succeeds, else sigattn_bwd (the recompute kernels)."""
+    succeeds, else the recompute kernels: sigattn_bwd_split with its
+    workspace when a small dense grid splits (head_dim 64), sigattn_bwd
+    otherwise."""
     def run(stream):
         ws, nbytes = _bwd_workspace(bwd_workspace_bytes(lib, pr, dQ.device), dQ.device)
+        if nbytes == 0 and pr.D not in TWO_PASS_HEAD_DIMS:
+            ws, nbytes = _bwd_workspace(int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr))), dQ.device)
+            _raise(lib.sigattn_bwd_split(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws),
+                                         nbytes, stream), "sigattn_bwd_split")
+            return
         _raise(lib.sigattn_bwd_ws(ctypes.byref(pr), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(ws), nbytes,
                                   stream), "sigattn_bwd_ws")
 
