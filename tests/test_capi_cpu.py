@@ -48,6 +48,26 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
+def test_autograd_node_loads_and_binds_to_the_library():
+    """The C++ autograd node imports next to the library, binds to the
+    library's entry points (every name it asks for is a declared one) and
+    exposes attention(); calling it needs a GPU."""
+    import importlib
+
+    mod = importlib.import_module("triton_sigmoid._sigattn_autograd")
+    assert set(_capi._AUTOGRAD_FNS) <= set(_capi.SIGNATURES)
+    assert hasattr(mod, "attention") and hasattr(mod, "bind")
+    with pytest.raises(RuntimeError, match="missing sigattn_fwd_ws"):
+        mod.bind({"sigattn_strerror": 1, "sigattn_fwd_workspace_bytes": 1}, [128], 512)
+    node = _capi.autograd_node()
+    assert node is mod
+
+
+def test_eager_binding_env_selects_the_python_node(monkeypatch):
+    monkeypatch.setenv("SIGATTN_EAGER_BINDING", "python")
+    assert _capi.autograd_node() is None
+
+
 def test_abi_version_and_strerror():
     lib = _capi.load_library()
     assert lib.sigattn_abi_version() == _capi.ABI_VERSION

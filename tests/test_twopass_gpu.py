@@ -288,8 +288,12 @@ def test_public_api_uses_two_pass_at_d128(causal, monkeypatch):
 
 def test_workspace_allocation_failure_falls_back_to_recompute(monkeypatch):
     """When the dS workspace cannot be allocated the backward still runs (the
-    recompute kernels) and gives exactly the recompute backward's gradients."""
+    recompute kernels) and gives exactly the recompute backward's gradients.
+    The allocation is made to fail by patching torch.empty, so this runs the
+    Python autograd node; the C++ node's fallback is tested in
+    test_autograd_node_gpu.py with the device memory actually exhausted."""
     import triton_sigmoid as ts
+    monkeypatch.setenv("SIGATTN_EAGER_BINDING", "python")
     B, T, H, D = 2, 384, 4, 128
     dtype = torch.bfloat16
     q, k, v, do = _dense_case(B, T, H, D, dtype, seed=22)

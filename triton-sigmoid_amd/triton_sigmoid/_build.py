@@ -1,8 +1,12 @@
-"""Builds libsigattn.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+"""Builds libsigattn.so (the gfx950 kernels + C ABI) in-tree with hipcc, and
+the C++ autograd node of the eager public APIs (_sigattn_autograd) with g++.
 
 Every HIP source is compiled for gfx950 only, with packed-fp32 instruction
 selection disabled (``-Xclang -target-feature -Xclang -packed-fp32-ops``), and
-linked into ``triton_sigmoid/libsigattn.so`` next to this file.
+linked into ``triton_sigmoid/libsigattn.so`` next to this file.  The autograd
+node (csrc/torch_autograd.cpp) is host-only C++ against torch's headers and
+libraries; it calls libsigattn through entry point addresses handed over at
+run time, so it does not link the kernel library.
 """
 
 from __future__ import annotations
@@ -11,6 +15,7 @@ import concurrent.futures as _cf
 import os
 import shutil
 import subprocess
+import sysconfig
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -22,6 +27,8 @@ BUILD_DIR = ROOT / "_build"
 
 SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "capi.cpp"]
 ARCH = "gfx950"
+AUTOGRAD_SOURCE = "torch_autograd.cpp"
+AUTOGRAD_NAME = "_sigattn_autograd"
 
 
 def hipcc() -> str:
@@ -51,8 +58,40 @@ def _compile(src: Path, obj: Path, defines: tuple = ()) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
 
 
+def autograd_path() -> Path:
+    return PKG_DIR / (AUTOGRAD_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_autograd(out: Path | None = None) -> Path:
+    """Compiles the C++ autograd node into the package (or `out`)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    target = Path(out) if out is not None else autograd_path()
+    tmp = target.with_name(target.name + ".tmp")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={AUTOGRAD_NAME}",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           *(f"-I{p}" for p in cpp_extension.include_paths()),
+           f"-I{sysconfig.get_paths()['include']}", f"-I{_rocm_include()}",
+           str(CSRC / AUTOGRAD_SOURCE), "-o", str(tmp),
+           *(f"-L{p}" for p in cpp_extension.library_paths()),
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lamdhip64"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for {AUTOGRAD_SOURCE}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, target)
+    return target
+
+
+def _rocm_include() -> str:
+    return str(Path(os.path.realpath(hipcc())).parent.parent / "include")
+
+
 def build(verbose: bool = False, jobs: int = 4, defines: tuple = (), out: Path | None = None) -> Path:
     """Compiles every source and links LIB_PATH (or `out`).  Always rebuilds.
+    The default build also compiles the C++ autograd node (build_autograd).
 
     `defines` are extra -D options for the tile-configuration macros of the
     kernel sources (e.g. "-DSIGATTN_FWD_D64_STAGES=4"); a build with them
@@ -65,8 +104,10 @@ def build(verbose: bool = False, jobs: int = 4, defines: tuple = (), out: Path |
     bdir = BUILD_DIR if not defines else BUILD_DIR / ("variant_" + lib.stem)
     bdir.mkdir(parents=True, exist_ok=True)
     objs = [bdir / (Path(s).stem + ".o") for s in SOURCES]
-    with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+    with _cf.ThreadPoolExecutor(max_workers=jobs + 1) as ex:
         futs = [ex.submit(_compile, CSRC / s, o, defines) for s, o in zip(SOURCES, objs)]
+        if out is None:
+            futs.append(ex.submit(build_autograd))
         for f in futs:
             f.result()
     tmp = lib.with_suffix(".so.tmp")
@@ -76,7 +117,7 @@ def build(verbose: bool = False, jobs: int = 4, defines: tuple = (), out: Path |
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, lib)
     if verbose:
-        print(f"built {lib}")
+        print(f"built {lib}" + (f" and {autograd_path()}" if out is None else ""))
     return lib
 
 

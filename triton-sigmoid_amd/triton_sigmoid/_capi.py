@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import warnings
 from pathlib import Path
 from typing import Optional
 
@@ -115,6 +116,48 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+# C++ autograd node of the eager public APIs (csrc/torch_autograd.cpp,
+# _sigattn_autograd next to this file): the same kernels, launch policy,
+# saved tensors and gradients as the Python nodes (torch.autograd.Function
+# in the op modules) with far less host time per call, and a backward that
+# runs on the autograd engine's device thread without taking the GIL.  The
+# environment variable SIGATTN_EAGER_BINDING=python selects the Python nodes;
+# so does a node that fails to import (with a warning).
+_EAGER_ENV = "SIGATTN_EAGER_BINDING"
+_AUTOGRAD_FNS = ("sigattn_strerror", "sigattn_fwd_workspace_bytes", "sigattn_fwd_ws",
+                 "sigattn_bwd_workspace_bytes", "sigattn_bwd_ws", "sigattn_bwd_split_workspace_bytes",
+                 "sigattn_bwd_split")
+_autograd = None  # the bound module, or False after a failed import
+
+
+def autograd_node():
+    """The bound C++ autograd module, or None when the Python nodes serve."""
+    global _autograd
+    if os.environ.get(_EAGER_ENV, "").strip().lower() == "python":
+        return None
+    if _autograd is None:
+        lib = load_library()
+        try:
+            from . import _sigattn_autograd as mod
+        except ImportError as e:
+            warnings.warn(f"sigmoid attention: C++ autograd node not loaded ({e}); the Python node serves the "
+                          "eager APIs, with more host time per call")
+            _autograd = False
+            return None
+        mod.bind({n: ctypes.cast(getattr(lib, n), ctypes.c_void_p).value for n in _AUTOGRAD_FNS},
+                 list(TWO_PASS_HEAD_DIMS), _DQ_DS_ROWS)
+        _autograd = mod
+    return _autograd or None
+
+
+def attention_node(node, Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal) -> torch.Tensor:
+    """O with autograd through the C++ node on the canonical op inputs."""
+    Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k = _prepare(
+        Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k)
+    return node.attention(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, bool(causal),
+                          bwd_workspace_limit())
 
 
 def strerror(code: int) -> str:

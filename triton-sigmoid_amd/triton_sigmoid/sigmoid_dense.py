@@ -91,8 +91,9 @@ sigmoid_attention_fwd_op.register_autograd(_dense_backward, setup_context=_dense
 
 
 class _DenseEager(torch.autograd.Function):
-    """Eager-mode path of sigmoid_attention: the same kernels, saved tensors
-    and gradients as myops::sigmoid_attention_fwd with its registered autograd,
+    """Eager-mode path of sigmoid_attention when the C++ autograd node
+    (_capi.autograd_node) is not used: the same kernels, saved tensors and
+    gradients as myops::sigmoid_attention_fwd with its registered autograd,
     without the custom-op dispatch (which costs more host time per call than
     a small problem's kernels take).  torch.compile traces the registered op."""
 
@@ -176,5 +177,9 @@ def sigmoid_attention(
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
-    op = sigmoid_attention_fwd_op if torch.compiler.is_compiling() else _DenseEager.apply
-    return op(query, key, value, bias, score_mod, scale_tensor, is_causal)
+    if torch.compiler.is_compiling():
+        return sigmoid_attention_fwd_op(query, key, value, bias, score_mod, scale_tensor, is_causal)
+    node = _capi.autograd_node()
+    if node is not None:
+        return _capi.attention_node(node, query, key, value, bias, score_mod, scale_tensor, None, None, is_causal)
+    return _DenseEager.apply(query, key, value, bias, score_mod, scale_tensor, is_causal)

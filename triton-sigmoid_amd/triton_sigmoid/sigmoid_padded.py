@@ -93,7 +93,8 @@ sigmoid_attn_padded_fwd_op.register_autograd(_padded_backward, setup_context=_pa
 
 
 class _PaddedEager(torch.autograd.Function):
-    """Eager-mode path of sigmoid_attention_padded: the same kernels, saved
+    """Eager-mode path of sigmoid_attention_padded when the C++ autograd node
+    (_capi.autograd_node) is not used: the same kernels, saved
     tensors and gradients as myops::sigmoid_attn_padded_fwd with its
     registered autograd, without the custom-op dispatch.  torch.compile
     traces the registered op."""
@@ -197,5 +198,11 @@ def sigmoid_attention_padded(
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
-    op = sigmoid_attn_padded_fwd_op if torch.compiler.is_compiling() else _PaddedEager.apply
-    return op(query, key, value, seq_lens_k, seq_lens_q, bias, score_mod, scale_tensor, is_causal)
+    if torch.compiler.is_compiling():
+        return sigmoid_attn_padded_fwd_op(query, key, value, seq_lens_k, seq_lens_q, bias, score_mod, scale_tensor,
+                                          is_causal)
+    node = _capi.autograd_node()
+    if node is not None:
+        return _capi.attention_node(node, query, key, value, bias, score_mod, scale_tensor, seq_lens_q, seq_lens_k,
+                                    is_causal)
+    return _PaddedEager.apply(query, key, value, seq_lens_k, seq_lens_q, bias, score_mod, scale_tensor, is_causal)
