@@ -170,7 +170,8 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
     o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     # The forward the public API runs: with the workspace the library asks
-    # for (the split-KV kernel at decode shapes; none otherwise).
+    # for (the split-KV kernel at decode shapes, the range split of small
+    # dense grids; none otherwise).
     fbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
     fws = torch.empty(max(fbytes, 16), dtype=torch.uint8, device=q.device)
     calls = {"fwd": lambda: lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), fws.data_ptr() if fbytes else None,
@@ -185,9 +186,17 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         calls["bwd_dq"] = lambda: lib.sigattn_bwd_dq_ws(ctypes.byref(pr), dq.data_ptr(), ws.data_ptr(), nbytes,
                                                         stream)
     else:
-        calls["bwd_dq"] = lambda: lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream)
-        calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
-                                                         dv.data_ptr(), stream)
+        # The recompute kernels, range-split where the public API splits them
+        # (each half of sigattn_bwd_split on the whole workspace; the timing
+        # includes its counter-clearing launch).
+        nbytes = 0
+        sbytes = 0 if D in _capi.TWO_PASS_HEAD_DIMS else int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
+        sws = torch.empty(max(sbytes, 16), dtype=torch.uint8, device=q.device)
+        sptr = sws.data_ptr() if sbytes else None
+        calls["bwd_dq"] = lambda: lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), None, None,
+                                                        sptr, sbytes, stream)
+        calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), None, dk.data_ptr(),
+                                                          dv.data_ptr(), sptr, sbytes, stream)
     # Median of three timed runs of `iters` launches each: the first kernel
     # timed after a long step loop can read 10-20 % slow on its own.
     out = {}

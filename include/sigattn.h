@@ -170,7 +170,9 @@ int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
  * same launch.  sigattn_bwd_split_workspace_bytes(p) is the workspace it
  * needs (0 when nothing splits, or without a device); with workspace NULL
  * or when nothing splits, sigattn_bwd_split runs sigattn_bwd.  Results are
- * deterministic and equal sigattn_bwd's within fp32 summation order.
+ * deterministic and equal sigattn_bwd's within fp32 summation order.  With
+ * dq NULL (or dk and dv NULL) it runs only the other half, like
+ * sigattn_bwd_dkdv (sigattn_bwd_dq), on the same workspace size.
  */
 size_t sigattn_bwd_split_workspace_bytes(const sigattn_problem *p);
 int sigattn_bwd_split(const sigattn_problem *p, const void *dout, void *dq, void *dk, void *dv,

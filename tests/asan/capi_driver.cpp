@@ -72,7 +72,9 @@ int bwd_dq_rows_per_workgroup() { return 128; }
 int bwd_dkdv_rows_per_workgroup() { return 128; }
 int bwd_dq_workgroups_per_cu(int D) { return D == 64 ? 3 : 2; }
 int bwd_dkdv_workgroups_per_cu(int D) { return D == 64 ? 2 : 1; }
-void launch_rs_clear(int *, int, hipStream_t) { g_calls.emplace_back("rs_clear"); }
+void launch_rs_clear(int *, int na, int *, int nb, hipStream_t) {
+  if (na + nb > 0) g_calls.emplace_back("rs_clear");
+}
 // The fixed scratch of sigattn_fwd_noalloc: any aligned address stands in.
 hipError_t splitkv_scratch(float **ptr) {
   *ptr = reinterpret_cast<float *>(uintptr_t(3) << 20);
@@ -239,9 +241,19 @@ int main() {
     const size_t dq_bytes = 512 + size_t(128) * 2 * 128 * 64 * 4;
     EXPECT(bw == dq_bytes + 512 + size_t(128) * 2 * 2 * 128 * 64 * 4);
     EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, kFake, bw, nullptr) == 0 &&
-           calls() == "rs_clear,rs_clear,dq_mfma,dkdv_mfma");
+           calls() == "rs_clear,dq_mfma,dkdv_mfma");
     EXPECT(g_last.rsplit == 2 && (char *)g_last.rs_cnt == (char *)kFake + dq_bytes);
     EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, kFake, bw - 1, nullptr) == SIGATTN_ERR_WORKSPACE);
+    // Halves: dQ alone, dK/dV alone (its counters after dQ's part), neither.
+    EXPECT(sigattn_bwd_split(&p, kFake, kFake, nullptr, nullptr, kFake, bw, nullptr) == 0 &&
+           calls() == "rs_clear,dq_mfma" && g_last.rsplit == 2 && g_last.rs_cnt == kFake);
+    EXPECT(sigattn_bwd_split(&p, kFake, nullptr, kFake, kFake, kFake, bw, nullptr) == 0 &&
+           calls() == "rs_clear,dkdv_mfma" && (char *)g_last.rs_cnt == (char *)kFake + dq_bytes);
+    EXPECT(sigattn_bwd_split(&p, kFake, nullptr, nullptr, nullptr, kFake, bw, nullptr) == SIGATTN_ERR_NULL_ARG &&
+           g_calls.empty());
+    EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, nullptr, kFake, bw, nullptr) == SIGATTN_ERR_NULL_ARG);
+    EXPECT(sigattn_bwd_split(&p, kFake, nullptr, kFake, kFake, nullptr, 0, nullptr) == 0 &&
+           calls() == "dkdv_mfma" && g_last.rsplit == 0);
     EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, nullptr, 0, nullptr) == 0 &&
            calls() == "dq_mfma,dkdv_mfma" && g_last.rsplit == 0);
     // Causal, padded, D = 128 backward, or grids that fill the GPU: no split.

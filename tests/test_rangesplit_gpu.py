@@ -200,6 +200,27 @@ def test_backward_split_repeats_bitwise_with_score_mod():
         assert_close_to_oracle(a, want, dtype, name)
 
 
+def test_backward_split_halves_equal_the_whole():
+    """dQ alone (dk, dv NULL) and dK/dV alone (dq NULL) on the same workspace
+    give the whole call's bits."""
+    q, k, v, do = _case(2, 1100, 2, 64, torch.bfloat16, seed=61)
+    bias, scale = _scalars(2, 1100, 64)
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
+    lib = _capi.load_library()
+    nbytes = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
+    assert nbytes > 0
+    ws = _nan_workspace(nbytes)
+    whole = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd_split(pr, do, *whole, ws=ws, nbytes=nbytes)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)
+    for args in ((dq.data_ptr(), None, None), (None, dk.data_ptr(), dv.data_ptr())):
+        rc = lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), *args, ws.data_ptr(), nbytes, _stream())
+        assert rc == 0, _capi.strerror(rc)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), (dq, dk, dv), whole):
+        assert torch.equal(a, b), f"{name}: half call differs from the whole"
+
+
 def test_workspace_too_small_is_rejected():
     q, k, v, do = _case(1, 1024, 2, 64, torch.float16, seed=31)
     bias, scale = _scalars(1, 1024, 64)

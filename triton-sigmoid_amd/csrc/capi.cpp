@@ -198,13 +198,12 @@ BwdSplit bwd_range_split(const sigattn_problem *p, bool mfma) {
   return s;
 }
 
-// Sets k's range-split fields for `r` over the workspace at `ws` and clears
-// its counters on `st`.
-void use_range_split(KParams &k, const RangeSplit &r, void *ws, hipStream_t st) {
+// Sets k's range-split fields for `r` over the workspace at `ws`; the caller
+// clears the counters (launch_rs_clear) before k's kernel runs.
+void use_range_split(KParams &k, const RangeSplit &r, void *ws) {
   k.rsplit = r.n;
   k.rs_cnt = (int *)ws;
   k.rs_part = (float *)((char *)ws + r.cnt_bytes);
-  sigattn::launch_rs_clear(k.rs_cnt, (int)r.items, st);
 }
 
 // Two-pass backward: bytes of dS tiles (DsLayout) per head, over all batches.
@@ -344,7 +343,10 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     if (rs.n > 1 && ((size_t)rs.bytes > workspace_bytes || !aligned16(workspace))) return SIGATTN_ERR_WORKSPACE;
   }
   (void)hipGetLastError();
-  if (rs.n > 1) use_range_split(k, rs, workspace, st);
+  if (rs.n > 1) {
+    use_range_split(k, rs, workspace);
+    sigattn::launch_rs_clear(k.rs_cnt, (int)rs.items, nullptr, 0, st);
+  }
   if (sp.nsplit > 0) {
     k.nsplit = sp.nsplit;
     k.chunk = sp.chunk;
@@ -471,11 +473,16 @@ int sigattn_bwd_split(const sigattn_problem *p, const void *dout, void *dq, void
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
   if (p->B == 0 || p->H == 0) return SIGATTN_OK;
+  // dq alone, or dk and dv alone, ask for that half of the backward.
+  const bool want_dq = dq != nullptr, want_kv = dk != nullptr || dv != nullptr;
+  if (!want_dq && !want_kv) return SIGATTN_ERR_NULL_ARG;
+  if (want_kv && (dk == nullptr || dv == nullptr)) return SIGATTN_ERR_NULL_ARG;
+  const BwdParts parts = want_dq && want_kv ? kBwdAll : (want_dq ? kBwdDq : kBwdDkdv);
   const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
   const BwdSplit bs = workspace != nullptr ? bwd_range_split(p, use_mfma(p, ptrs, 7)) : BwdSplit{};
-  if (bs.bytes == 0) return bwd_impl(p, dout, dq, dk, dv, nullptr, 0, stream, kBwdAll);
+  if (bs.bytes == 0) return bwd_impl(p, dout, dq, dk, dv, nullptr, 0, stream, parts);
   if ((size_t)bs.bytes > workspace_bytes || !aligned16(workspace)) return SIGATTN_ERR_WORKSPACE;
-  if (dq == nullptr || dk == nullptr || dv == nullptr || dout == nullptr) return SIGATTN_ERR_NULL_ARG;
+  if (dout == nullptr) return SIGATTN_ERR_NULL_ARG;
   KParams k = make_params(p);
   k.dout = dout;
   k.dq = dq;
@@ -484,11 +491,14 @@ int sigattn_bwd_split(const sigattn_problem *p, const void *dout, void *dq, void
   const hipStream_t st = (hipStream_t)stream;
   const bool sm = p->score_mod != nullptr;
   (void)hipGetLastError();
+  // Both kernels' counters are cleared by one launch ahead of them.
   KParams kq = k, kk = k;
-  if (bs.dq.n > 1) use_range_split(kq, bs.dq, workspace, st);
-  if (bs.kv.n > 1) use_range_split(kk, bs.kv, (char *)workspace + bs.dq.bytes, st);
-  sigattn::launch_bwd_dq_mfma(kq, p->dtype, (int)p->D, false, sm, st);
-  sigattn::launch_bwd_dkdv_mfma(kk, p->dtype, (int)p->D, false, sm, false, st);
+  if (want_dq && bs.dq.n > 1) use_range_split(kq, bs.dq, workspace);
+  if (want_kv && bs.kv.n > 1) use_range_split(kk, bs.kv, (char *)workspace + bs.dq.bytes);
+  sigattn::launch_rs_clear(kq.rs_cnt, kq.rsplit > 1 ? (int)bs.dq.items : 0, kk.rs_cnt,
+                           kk.rsplit > 1 ? (int)bs.kv.items : 0, st);
+  if (want_dq) sigattn::launch_bwd_dq_mfma(kq, p->dtype, (int)p->D, false, sm, st);
+  if (want_kv) sigattn::launch_bwd_dkdv_mfma(kk, p->dtype, (int)p->D, false, sm, false, st);
   return launch_status();
 }
 

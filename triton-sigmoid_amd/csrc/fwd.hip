@@ -488,11 +488,15 @@ static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStrea
 int fwd_rows_per_workgroup(int D) { return (D == 64 ? 4 : 8) * 32; }
 int fwd_workgroups_per_cu(int D) { return D == 64 ? fwd_occupancy<64>() : fwd_occupancy<128>(); }
 
-__global__ __launch_bounds__(256) void rs_clear_kernel(int *cnt, int n) {
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) cnt[i] = 0;
+__global__ __launch_bounds__(256) void rs_clear_kernel(int *a, int na, int *b, int nb) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < na + nb; i += gridDim.x * 256) {
+    if (i < na) a[i] = 0;
+    else b[i - na] = 0;
+  }
 }
-void launch_rs_clear(int *cnt, int n, hipStream_t st) {
-  if (n > 0) rs_clear_kernel<<<(unsigned)min((n + 255) / 256, 64), 256, 0, st>>>(cnt, n);
+void launch_rs_clear(int *a, int na, int *b, int nb, hipStream_t st) {
+  const int n = na + nb;
+  if (n > 0) rs_clear_kernel<<<(unsigned)min((n + 255) / 256, 64), 256, 0, st>>>(a, na, b, nb);
 }
 
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,

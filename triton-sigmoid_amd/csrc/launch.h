@@ -21,9 +21,9 @@ int bwd_dq_rows_per_workgroup();
 int bwd_dkdv_rows_per_workgroup();
 int bwd_dq_workgroups_per_cu(int D);
 int bwd_dkdv_workgroups_per_cu(int D);
-// Zeroes n range-split arrival counters on `st` (a kernel: no memset node
-// lands in a captured graph).
-void launch_rs_clear(int *cnt, int n, hipStream_t st);
+// Zeroes two arrays of range-split arrival counters (na at a, nb at b) in
+// one launch on `st` (a kernel: no memset node lands in a captured graph).
+void launch_rs_clear(int *a, int na, int *b, int nb, hipStream_t st);
 
 // MFMA kernels: dtype in {kF16, kBF16}, D in {64, 128}, 16-byte aligned rows.
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
