@@ -144,7 +144,10 @@ int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t 
  * held until the process ends; its address is looked up on the first call on
  * each device (which must be current).  Every split plan fits (partials stay
  * below 16 MiB); a larger need returns SIGATTN_ERR_SCRATCH.  Other problems
- * run exactly as in sigattn_fwd.  Results equal sigattn_fwd_ws's bit for bit.
+ * run exactly as in sigattn_fwd, without the range split of small dense
+ * grids.  Results equal sigattn_fwd_ws's bit for bit, except on problems
+ * that sigattn_fwd_ws range-splits, where they equal sigattn_fwd's bit for
+ * bit and sigattn_fwd_ws's within fp32 summation order.
  * All calls on one GPU share its array: calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller.
  */

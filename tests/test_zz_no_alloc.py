@@ -66,6 +66,24 @@ def test_noalloc_matches_workspace_entry_point_on_two_calls():
         assert_close_to_oracle(got, o, dtype, f"O (call {i})")
 
 
+def test_noalloc_runs_range_split_problems_unsplit():
+    """A small dense non-causal grid that sigattn_fwd_ws range-splits runs
+    unsplit here: sigattn_fwd's bits."""
+    lib = _capi.load_library()
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn((1, 1024, 2, 64), generator=g).to("cuda", torch.float16) for _ in range(3))
+    bias = torch.full((1,), -math.log(1024), dtype=torch.float32, device="cuda")
+    scale = torch.full((), 0.125, dtype=torch.float32, device="cuda")
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
+    assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)) > 0
+    want, got = torch.empty_like(q), torch.empty_like(q)
+    assert lib.sigattn_fwd(ctypes.byref(pr), want.data_ptr(), stream) == 0
+    assert lib.sigattn_fwd_noalloc(ctypes.byref(pr), got.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_noalloc_runs_unsplit_problems_like_sigattn_fwd():
     lib = _capi.load_library()
     stream = torch.cuda.current_stream().cuda_stream
