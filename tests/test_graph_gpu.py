@@ -1,8 +1,9 @@
 """A whole forward + backward step captured in a HIP graph (torch.cuda.graph)
 and replayed: every replay must reproduce the eager step bit for bit.  The
 step allocates (outputs, gradients, the two-pass backward's dS workspace,
-the default bias and scale tensors) and launches the library's kernels on the
-capturing stream; none of it may be a host-side shortcut that a replay skips."""
+the range split's partials, the default bias and scale tensors) and launches
+the library's kernels on the capturing stream; none of it may be a host-side
+shortcut that a replay skips."""
 
 import pytest
 import torch
@@ -20,13 +21,19 @@ def _case(kind):
         B, T, H, D, dtype = 2, 320, 4, 128, torch.bfloat16
         q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
         return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v, is_causal=True)
+    if kind == "dense_d64_range_split":
+        # A small dense non-causal grid: forward, dQ and dK/dV range-split,
+        # their arrival counters cleared by a captured kernel each replay.
+        B, T, H, D, dtype = 1, 1100, 2, 64, torch.float16
+        q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
+        return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v)
     B, T, H, D, dtype = 3, 200, 2, 64, torch.float16
     q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
     sl = torch.tensor([200, 77, 130], dtype=torch.int32, device=DEV)
     return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl)
 
 
-@pytest.mark.parametrize("kind", ["dense_d128_causal", "padded_d64"])
+@pytest.mark.parametrize("kind", ["dense_d128_causal", "dense_d64_range_split", "padded_d64"])
 def test_graph_replays_match_eager(kind):
     (q, k, v, do), attn = _case(kind)
     leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
