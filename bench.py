@@ -176,9 +176,13 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
     fws = torch.empty(max(fbytes, 16), dtype=torch.uint8, device=q.device)
     calls = {"fwd": lambda: lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), fws.data_ptr() if fbytes else None,
                                                fbytes, stream)}
-    # The backward the public API runs: two-pass (dK/dV storing dS, then dQ
+    # The backward the public API runs: the range-split recompute kernels
+    # where a small grid splits, else two-pass (dK/dV storing dS, then dQ
     # from dS) where _capi uses it, else the recompute kernels.
-    nbytes = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))) if D in _capi.TWO_PASS_HEAD_DIMS else 0
+    sbytes = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
+    nbytes = 0
+    if sbytes == 0 and D in _capi.TWO_PASS_HEAD_DIMS:
+        nbytes = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
     if 0 < nbytes <= _capi.bwd_workspace_limit():
         ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         calls["bwd_dkdv"] = lambda: lib.sigattn_bwd_dkdv_ws(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(),
@@ -190,7 +194,6 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         # (each half of sigattn_bwd_split on the whole workspace; the timing
         # includes its counter-clearing launch).
         nbytes = 0
-        sbytes = 0 if D in _capi.TWO_PASS_HEAD_DIMS else int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
         sws = torch.empty(max(sbytes, 16), dtype=torch.uint8, device=q.device)
         sptr = sws.data_ptr() if sbytes else None
         calls["bwd_dq"] = lambda: lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), None, None,

@@ -165,10 +165,10 @@ int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
 /*
  * The recompute backward with the range split of small dense grids (no
  * counterpart in the reference): for a dense non-causal problem at head_dim
- * 64 taking the MFMA kernels, whose dQ or dK/dV grid would leave at least
- * half of the GPU's compute units idle, the dQ kernel runs each query
- * block's keys and the dK/dV kernel each key block's queries as 2-4 chunks
- * of at least 512 rows (so T >= 1024), the fp32
+ * 64 or 128 taking the MFMA kernels, whose dQ or dK/dV grid would leave at
+ * least half of the GPU's compute units idle, the dQ kernel runs each query
+ * block's keys and (head_dim 64) the dK/dV kernel each key block's queries
+ * as 2-4 chunks of at least 512 rows (so T >= 1024), the fp32
  * partials added in chunk order by the last chunk to finish, inside the
  * same launch.  sigattn_bwd_split_workspace_bytes(p) is the workspace it
  * needs (0 when nothing splits, or without a device); with workspace NULL

@@ -263,8 +263,12 @@ int main() {
     c = p;
     c.seq_lens_q = c.seq_lens_k = (const int32_t *)kFake;
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    // D = 128: the forward and the dQ kernel split, the dK/dV kernel does not.
     c = base(2, 1024, 8, 128);
-    EXPECT(sigattn_fwd_workspace_bytes(&c) > 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    const size_t bw128 = sigattn_bwd_split_workspace_bytes(&c);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) > 0 && bw128 == 512 + size_t(128) * 2 * 128 * 128 * 4);
+    EXPECT(sigattn_bwd_split(&c, kFake, kFake, kFake, kFake, kFake, bw128, nullptr) == 0 &&
+           calls() == "rs_clear,dq_mfma,dkdv_mfma" && g_last.rsplit == 0);
     c = base(4, 1024, 8, 64);  // 256 items: the GPU is already half full
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
     c = base(2, 1000, 8, 64);  // keys too few for two chunks of 512

@@ -55,6 +55,7 @@ DENSE = [  # (B, T, H, D, dtype, causal)
     (2, 1024, 8, 64, torch.float16, False),   # c2: range split forward and backward
     (2, 1024, 8, 64, torch.float16, True),
     (2, 384, 4, 128, torch.bfloat16, False),  # two-pass backward
+    (1, 2048, 2, 128, torch.bfloat16, False), # range split forward and dQ
     (1, 300, 3, 128, torch.bfloat16, True),
     (2, 77, 2, 32, torch.float32, False),     # portable kernels
     (1, 16, 2, 64, torch.bfloat16, False),    # decode-sized queries

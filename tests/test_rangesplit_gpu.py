@@ -150,16 +150,18 @@ def test_forward_split_repeats_bitwise_and_reuses_its_workspace():
     _assert_fp32_order(got, ref, dtype, "O (second problem)")
 
 
-BWD_SHAPES = [(1, 1024, 2), (2, 1100, 2), (1, 1700, 1), (1, 2100, 1)]
+# (B, T, H, D): at D = 64 the dQ and dK/dV kernels split, at D = 128 the dQ
+# kernel (the dK/dV kernel runs one key block per workgroup).
+BWD_SHAPES = [(1, 1024, 2, 64), (2, 1100, 2, 64), (1, 1700, 1, 64), (1, 2100, 1, 64), (1, 1100, 2, 128),
+              (1, 2100, 1, 128)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_backward_split_matches_oracle_and_unsplit(shape, dtype):
-    B, T, H = shape
-    D = 64
+    B, T, H, D = shape
     print(f"backward split {shape} {dtype}", flush=True)
-    q, k, v, do = _case(B, T, H, D, dtype, seed=3 * T + H)
+    q, k, v, do = _case(B, T, H, D, dtype, seed=3 * T + H + D)
     bias, scale = _scalars(B, T, D)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()

@@ -19,6 +19,7 @@
 // with the MFMA chains of the next; the dQ kernel (two waves per SIMD) relies
 // on the second wave for that overlap.  Rows past seq_lens are fetched as
 // copies of the last valid row (in bounds) and masked on boundary tiles.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -665,7 +666,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
   // order.  Dense problems take key blocks j and nblk-1-j in sequence
   // (grid = ceil(nblk/2) per (batch, head)): under the causal mask the two
   // together cost the same for every j, so all workgroups are equal, and
-  // the grid has half as many workgroup starts.
+  // the grid has half as many workgroup starts.  A dense non-causal grid
+  // that would not fill the GPU paired runs one key block per workgroup
+  // (grid = nblk per (batch, head)).
   int b, h, kblk0, nitems;
   if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
@@ -677,7 +680,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
     const int BH = p.B * p.H;
     int bh;
     dense_item(blockIdx.x, BH, (int)(gridDim.x / BH), !CAUSAL || kDkdvGrouped, bh, kblk0);
-    nitems = p.nblk - 1 - kblk0 > kblk0 ? 2 : 1;
+    const bool paired = (int)(gridDim.x / BH) < p.nblk;
+    nitems = paired && p.nblk - 1 - kblk0 > kblk0 ? 2 : 1;
     b = bh / p.H, h = bh % p.H;
   }
   for (int item = 0; item < nitems; ++item) {
@@ -1259,12 +1263,29 @@ static void bwd_dq_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   });
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+static int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <typename T, int D, bool DSOUT>
 static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   launch_rows<128>(kp, kp.Tk, [&](const KParams &p, dim3 grid) {
     if constexpr (D == 128) {
-      // Dense problems: two key blocks per workgroup (see the kernel).
-      if (!(p.ragged() && p.B <= 64)) grid = dim3((unsigned)(((p.nblk + 1) / 2) * p.B * p.H));
+      // Dense problems: two key blocks per workgroup (see the kernel), or
+      // one when a non-causal grid of pairs would not fill the GPU.
+      if (!(p.ragged() && p.B <= 64)) {
+        const int64_t paired = (int64_t)((p.nblk + 1) / 2) * p.B * p.H;
+        grid = dim3((unsigned)(!causal && paired < device_cu_count() ? (int64_t)p.nblk * p.B * p.H : paired));
+      }
       if (causal) {
         if (sm) bwd_dkdv_pair_kernel<T, true, true, DSOUT><<<grid, 512, 0, st>>>(p);
         else bwd_dkdv_pair_kernel<T, true, false, DSOUT><<<grid, 512, 0, st>>>(p);

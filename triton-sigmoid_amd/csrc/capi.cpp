@@ -178,8 +178,9 @@ RangeSplit fwd_range_split(const sigattn_problem *p, bool mfma) {
                      (int64_t)BM * D);
 }
 
-// The recompute backward's split (D = 64, whose backward is the recompute
-// one): the dQ kernel splits keys, the dK/dV kernel queries.
+// The recompute backward's split: the dQ kernel splits keys, the D = 64
+// dK/dV kernel queries (the D = 128 one runs unsplit, with one key block per
+// workgroup when pairs would not fill the GPU).
 struct BwdSplit {
   RangeSplit dq, kv;
   int64_t bytes = 0;
@@ -187,13 +188,14 @@ struct BwdSplit {
 
 BwdSplit bwd_range_split(const sigattn_problem *p, bool mfma) {
   BwdSplit s;
-  if (!splittable(p, mfma) || p->D != 64) return s;
-  const int D = 64, cus = device_cus();
+  if (!splittable(p, mfma) || (p->D != 64 && p->D != 128)) return s;
+  const int D = (int)p->D, cus = device_cus();
   const int RQ = sigattn::bwd_dq_rows_per_workgroup(), RK = sigattn::bwd_dkdv_rows_per_workgroup();
   s.dq = range_split(p->B * p->H * cdiv(p->Tq, RQ), cus, sigattn::bwd_dq_workgroups_per_cu(D), p->Tk,
                      (int64_t)RQ * D);
-  s.kv = range_split(p->B * p->H * cdiv(p->Tk, RK), cus, sigattn::bwd_dkdv_workgroups_per_cu(D), p->Tq,
-                     2 * (int64_t)RK * D);
+  if (D == 64)
+    s.kv = range_split(p->B * p->H * cdiv(p->Tk, RK), cus, sigattn::bwd_dkdv_workgroups_per_cu(D), p->Tq,
+                       2 * (int64_t)RK * D);
   s.bytes = s.dq.bytes + s.kv.bytes;
   return s;
 }

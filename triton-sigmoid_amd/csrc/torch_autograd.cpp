@@ -12,11 +12,12 @@
 // prepared and saves them; the backward launches the library's backward on
 // them.  Launch policy is the Python layer's (_capi._launch_fwd,
 // _capi._launch_bwd): the forward passes the workspace
-// sigattn_fwd_workspace_bytes asks for; the backward takes the two-pass
-// kernels at the head dims and workspace limit the Python layer configures
-// (in head groups when the whole problem's dS does not fit, unless a group's
+// sigattn_fwd_workspace_bytes asks for; the backward takes the range-split
+// recompute backward when a small grid splits, else the two-pass kernels at
+// the head dims and workspace limit the Python layer configures (in head
+// groups when the whole problem's dS does not fit, unless a group's
 // dQ-from-dS grid would have fewer workgroups than the GPU has compute
-// units), else the range-split recompute backward.  Workspaces come from
+// units), else the recompute backward.  Workspaces come from
 // torch's caching allocator; a workspace that cannot be allocated falls back
 // to the kernels that need none.
 //
@@ -182,14 +183,15 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
     const hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
     bool two_pass = false;
     for (int64_t d : g_two_pass_dims) two_pass |= d == p.D;
-    Tensor ws = workspace(two_pass_bytes(p, limit, dev), q);
-    if (!ws.defined() && !two_pass) {
-      ws = workspace((int64_t)g_api.bwd_split_workspace_bytes(&p), q);
+    const int64_t split = (int64_t)g_api.bwd_split_workspace_bytes(&p);
+    if (split > 0 || !two_pass) {
+      const Tensor ws = workspace(split, q);
       check_rc(g_api.bwd_split(&p, dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0, stream),
                "sigattn_bwd_split");
       return result;
     }
+    const Tensor ws = workspace(two_pass_bytes(p, limit, dev), q);
     check_rc(g_api.bwd_ws(&p, dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                           ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0, stream),
              "sigattn_bwd_ws");
