@@ -18,7 +18,9 @@ padding rows filled with N(0,1) noise; FLOPs count only valid (query, key)
 pairs, and the same run times the dense kernels at the full shape to report
 the padded path's TFLOPS per valid token as a fraction of dense.  The default
 run (c3) measures c4 and c5 the same way after the headline and reports them
-under "padded" in the same JSON line (--no-padded skips them).
+under "padded" in the same JSON line (--no-padded skips them), and the step
+time of BASELINE.json configs[1] (dense fp16 B=2 L=1024 H=8 D=64, non-causal
+c2 and causal c2c) under "small" (--no-small skips it).
 
 Prints ONE JSON line on stdout; details go to stderr.
 """
@@ -578,6 +580,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-padded", action="store_true",
                     help="with the default c3 config: skip the c4 / c5 padded-vs-dense measurements")
+    ap.add_argument("--no-small", action="store_true",
+                    help="with the default c3 config: skip the c2 / c2c small-problem step measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--sweep", action="store_true",
@@ -659,6 +663,18 @@ def main():
                                 step_pct_of_peak=round(100 * r["fb_tflops"] / PEAK_BF16_TFLOPS, 2),
                                 workload=workload_name(name, CONFIGS[name]))
 
+    # BASELINE configs[1] (dense fp16 B=2 L=1024 H=8 D=64, non-causal and
+    # causal) rides along too: a small problem whose step time is set by the
+    # host path and the grid's fill of the GPU as much as by the kernels.
+    small = {}
+    if args.config == "c3" and not args.no_small:
+        for name in ("c2", "c2c"):
+            torch.cuda.empty_cache()
+            r = measure_config(name, max(args.steps, 200), args.warmup)
+            small[name] = dict(step_ms=round(r["ms_step"], 4), step_tflops=round(r["fb_tflops"], 2),
+                               kernel_ms={n: round(t, 4) for n, t in r["kernel_ms"].items()},
+                               workload=workload_name(name, CONFIGS[name]))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(res["cfg"])
@@ -700,6 +716,8 @@ def main():
     }
     if padded:
         line["padded"] = padded
+    if small:
+        line["small"] = small
     print(json.dumps(line), flush=True)
 
 
