@@ -1,7 +1,7 @@
 """GPU tests of the C++ autograd node of the eager public APIs
 (_sigattn_autograd, csrc/torch_autograd.cpp).  It launches the same kernels
 with the same workspace policy as the Python nodes (torch.autograd.Function
-in sigmoid_dense.py / sigmoid_padded.py, selected by
+in sigmoid_dense.py / sigmoid_padded.py / sigmoid_varlen.py, selected by
 SIGATTN_EAGER_BINDING=python), so outputs and gradients must be bitwise
 equal to theirs; the Python nodes are checked against the oracle by the
 other GPU tests.  The reference's eager path is the Python autograd of
@@ -91,6 +91,26 @@ def test_padded_matches_python_node(D, causal, monkeypatch):
                                                      is_causal=causal)
     _assert_same(_run(fn, (q, k, v), do, "cpp", monkeypatch), _run(fn, (q, k, v), do, "python", monkeypatch),
                  f"padded D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_varlen_matches_python_node(D, causal, monkeypatch):
+    """Packed sequences ([rows, H, D] with cu_seqlens, given as int32 and
+    int64), one of a single key."""
+    lens_q, lens_k = [300, 17, 250], [420, 33, 1]
+    cu_q = torch.tensor([0, 300, 317, 567], dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0, 420, 453, 454], dtype=torch.int64, device=DEV)
+    g = torch.Generator().manual_seed(D + causal)
+    H, dtype = 2, torch.bfloat16
+    q = randn((567, H, D), dtype, DEV, g)
+    k = randn((454, H, D), dtype, DEV, g)
+    v = randn((454, H, D), dtype, DEV, g)
+    do = randn((567, H, D), dtype, DEV, g)
+    fn = lambda q, k, v: ts.sigmoid_attention_varlen(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k),  # noqa: E731
+                                                     is_causal=causal)
+    _assert_same(_run(fn, (q, k, v), do, "cpp", monkeypatch), _run(fn, (q, k, v), do, "python", monkeypatch),
+                 f"varlen D={D} causal={causal}")
 
 
 @pytest.mark.parametrize("mb", ["2048", "0", "600", "100"])

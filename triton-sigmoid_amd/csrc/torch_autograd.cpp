@@ -1,5 +1,5 @@
 // Eager autograd node of the public APIs (sigmoid_attention,
-// sigmoid_attention_padded), in C++.
+// sigmoid_attention_padded, sigmoid_attention_varlen), in C++.
 //
 // The reference builds its eager path from torch.autograd.Function-style
 // registrations in Python (src/triton_sigmoid/sigmoid_triton_dense.py:696-753,
@@ -73,34 +73,58 @@ int32_t dtype_code(const Tensor &t) {
 
 const void *ptr_or_null(const Tensor &t) { return t.defined() ? t.data_ptr() : nullptr; }
 
-// The problem over canonical tensors: Q/K/V contiguous [B, T, H, D], fp32
-// bias / scale / score_mod and int32 seq_lens on Q's device (or undefined).
+// The sequence layout: seq_lens (padded [B, T, H, D], or undefined for
+// dense) or cu_seqlens (packed [rows, H, D], with the longest sequences).
+struct Layout {
+  Tensor slq, slk, cuq, cuk;
+  int64_t max_q = 0, max_k = 0;
+  bool packed() const { return cuq.defined(); }
+};
+
+// The problem over canonical tensors: Q/K/V contiguous, fp32 bias / scale /
+// score_mod and int32 seq_lens / cu_seqlens on Q's device (or undefined).
 sigattn_problem make_problem(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &bias,
-                             const Tensor &score_mod, const Tensor &scale, const Tensor &slq, const Tensor &slk,
-                             bool causal) {
+                             const Tensor &score_mod, const Tensor &scale, const Layout &lay, bool causal) {
   sigattn_problem p;
   std::memset(&p, 0, sizeof(p));
   p.abi_version = SIGATTN_ABI_VERSION;
   p.dtype = dtype_code(q);
-  p.B = q.size(0);
-  p.Tq = q.size(1);
-  p.Tk = k.size(1);
-  p.H = q.size(2);
-  p.D = q.size(3);
-  p.q_stride_b = q.stride(0);
-  p.q_stride_t = q.stride(1);
-  p.q_stride_h = q.stride(2);
-  p.k_stride_b = k.stride(0);
-  p.k_stride_t = k.stride(1);
-  p.k_stride_h = k.stride(2);
+  if (lay.packed()) {
+    // An axis with no rows has no valid positions whatever max_seqlen says.
+    p.B = lay.cuq.numel() - 1;
+    p.Tq = q.size(0) > 0 ? lay.max_q : 0;
+    p.Tk = k.size(0) > 0 ? lay.max_k : 0;
+    p.H = q.size(1);
+    p.D = q.size(2);
+    p.q_stride_t = q.stride(0);
+    p.q_stride_h = q.stride(1);
+    p.k_stride_t = k.stride(0);
+    p.k_stride_h = k.stride(1);
+    p.cu_seqlens_q = static_cast<const int32_t *>(lay.cuq.data_ptr());
+    p.cu_seqlens_k = static_cast<const int32_t *>(lay.cuk.data_ptr());
+    p.rows_q = q.size(0);
+    p.rows_k = k.size(0);
+  } else {
+    p.B = q.size(0);
+    p.Tq = q.size(1);
+    p.Tk = k.size(1);
+    p.H = q.size(2);
+    p.D = q.size(3);
+    p.q_stride_b = q.stride(0);
+    p.q_stride_t = q.stride(1);
+    p.q_stride_h = q.stride(2);
+    p.k_stride_b = k.stride(0);
+    p.k_stride_t = k.stride(1);
+    p.k_stride_h = k.stride(2);
+    p.seq_lens_q = static_cast<const int32_t *>(ptr_or_null(lay.slq));
+    p.seq_lens_k = static_cast<const int32_t *>(ptr_or_null(lay.slk));
+  }
   p.q = q.data_ptr();
   p.k = k.data_ptr();
   p.v = v.data_ptr();
   p.bias = static_cast<const float *>(ptr_or_null(bias));
   p.scale = static_cast<const float *>(ptr_or_null(scale));
   p.score_mod = static_cast<const float *>(ptr_or_null(score_mod));
-  p.seq_lens_q = static_cast<const int32_t *>(ptr_or_null(slq));
-  p.seq_lens_k = static_cast<const int32_t *>(ptr_or_null(slk));
   p.causal = causal ? 1 : 0;
   return p;
 }
@@ -146,16 +170,20 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
   static Tensor forward(AutogradContext *ctx, const Tensor &q, const Tensor &k, const Tensor &v,
                         const Tensor &bias, const std::optional<Tensor> &score_mod, const Tensor &scale,
                         const std::optional<Tensor> &seq_lens_q, const std::optional<Tensor> &seq_lens_k,
-                        bool causal, int64_t bwd_limit) {
-    const Tensor sm = score_mod.value_or(Tensor()), slq = seq_lens_q.value_or(Tensor()),
-                 slk = seq_lens_k.value_or(Tensor());
-    ctx->save_for_backward({q, k, v, bias, scale, sm, slq, slk});
+                        bool causal, int64_t bwd_limit, const std::optional<Tensor> &cu_seqlens_q,
+                        const std::optional<Tensor> &cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k) {
+    const Tensor sm = score_mod.value_or(Tensor());
+    const Layout lay{seq_lens_q.value_or(Tensor()), seq_lens_k.value_or(Tensor()), cu_seqlens_q.value_or(Tensor()),
+                     cu_seqlens_k.value_or(Tensor()), max_seqlen_q, max_seqlen_k};
+    ctx->save_for_backward({q, k, v, bias, scale, sm, lay.slq, lay.slk, lay.cuq, lay.cuk});
     ctx->saved_data["causal"] = causal;
     ctx->saved_data["bwd_limit"] = bwd_limit;
+    ctx->saved_data["max_seqlen_q"] = max_seqlen_q;
+    ctx->saved_data["max_seqlen_k"] = max_seqlen_k;
     Tensor out = at::empty_like(q);
-    if (out.numel() == 0) return out;
+    if (out.numel() == 0 || (lay.packed() && lay.cuq.numel() == 1)) return out;
     const c10::DeviceGuard guard(q.device());
-    const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, slq, slk, causal);
+    const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, lay, causal);
     const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
     const int64_t nbytes = (int64_t)g_api.fwd_workspace_bytes(&p);
     Tensor ws = nbytes > 0 ? at::empty({nbytes}, q.options().dtype(at::kByte)) : Tensor();
@@ -167,7 +195,9 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
   static tensor_list backward(AutogradContext *ctx, tensor_list grads) {
     const auto saved = ctx->get_saved_variables();
     const Tensor &q = saved[0], &k = saved[1], &v = saved[2], &bias = saved[3], &scale = saved[4],
-                 &sm = saved[5], &slq = saved[6], &slk = saved[7];
+                 &sm = saved[5];
+    const Layout lay{saved[6], saved[7], saved[8], saved[9], ctx->saved_data["max_seqlen_q"].toInt(),
+                     ctx->saved_data["max_seqlen_k"].toInt()};
     const bool causal = ctx->saved_data["causal"].toBool();
     const int64_t limit = ctx->saved_data["bwd_limit"].toInt();
     Tensor dout = grads[0];
@@ -175,11 +205,12 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
       dout = dout.to(q.device(), q.scalar_type()).contiguous();
     TORCH_CHECK(dout.sizes() == q.sizes(), "dO shape ", dout.sizes(), " != Q shape ", q.sizes());
     Tensor dq = at::empty_like(q), dk = at::empty_like(k), dv = at::empty_like(v);
-    tensor_list result = {dq, dk, dv, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
-    if (dq.numel() == 0 && dk.numel() == 0) return result;
+    tensor_list result(14);
+    result[0] = dq, result[1] = dk, result[2] = dv;  // none for bias, score_mod, ... (no gradient)
+    if ((dq.numel() == 0 && dk.numel() == 0) || (lay.packed() && lay.cuq.numel() == 1)) return result;
     const c10::DeviceGuard guard(q.device());
     const int dev = q.device().index();
-    const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, slq, slk, causal);
+    const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, lay, causal);
     const hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
     bool two_pass = false;
     for (int64_t d : g_two_pass_dims) two_pass |= d == p.D;
@@ -202,9 +233,13 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
 Tensor attention(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &bias,
                  const std::optional<Tensor> &score_mod, const Tensor &scale,
                  const std::optional<Tensor> &seq_lens_q, const std::optional<Tensor> &seq_lens_k, bool causal,
-                 int64_t bwd_limit) {
+                 int64_t bwd_limit, const std::optional<Tensor> &cu_seqlens_q,
+                 const std::optional<Tensor> &cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k) {
   TORCH_CHECK(g_bound, "_sigattn_autograd: bind() was not called");
-  return SigattnNode::apply(q, k, v, bias, score_mod, scale, seq_lens_q, seq_lens_k, causal, bwd_limit);
+  TORCH_CHECK(cu_seqlens_q.has_value() == cu_seqlens_k.has_value(),
+              "_sigattn_autograd: cu_seqlens_q and cu_seqlens_k go together");
+  return SigattnNode::apply(q, k, v, bias, score_mod, scale, seq_lens_q, seq_lens_k, causal, bwd_limit,
+                            cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k);
 }
 
 template <class F> void bind_one(F &dst, const py::dict &fns, const char *name) {
@@ -234,7 +269,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "C++ autograd node of sigmoid_attention / sigmoid_attention_padded over libsigattn";
   m.def("bind", &bind, "Entry point addresses of libsigattn (name -> address), two-pass head dims, "
         "query rows per dQ-from-dS workgroup");
-  m.def("attention", &attention, "Forward with autograd; arguments are the canonical tensors of _capi._prepare",
+  m.def("attention", &attention,
+        "Forward with autograd; arguments are the canonical tensors of _capi._prepare (and _prepare_packed "
+        "for the packed layout, with the longest sequences)",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("bias"), py::arg("score_mod"), py::arg("scale"),
-        py::arg("seq_lens_q"), py::arg("seq_lens_k"), py::arg("causal"), py::arg("bwd_limit"));
+        py::arg("seq_lens_q"), py::arg("seq_lens_k"), py::arg("causal"), py::arg("bwd_limit"),
+        py::arg("cu_seqlens_q") = py::none(), py::arg("cu_seqlens_k") = py::none(), py::arg("max_seqlen_q") = 0,
+        py::arg("max_seqlen_k") = 0);
 }

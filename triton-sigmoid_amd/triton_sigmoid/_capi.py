@@ -160,6 +160,15 @@ def attention_node(node, Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_len
                           bwd_workspace_limit())
 
 
+def attention_node_packed(node, Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, bias,
+                          score_mod, sm_scale, causal) -> torch.Tensor:
+    """attention_node for packed [rows, H, D] tensors (cu_seqlens layout)."""
+    Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
+    cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
+    return node.attention(Q, K, V, bias, score_mod, sm_scale, None, None, bool(causal), bwd_workspace_limit(),
+                          cu_q, cu_k, int(max_seqlen_q), int(max_seqlen_k))
+
+
 def strerror(code: int) -> str:
     return load_library().sigattn_strerror(code).decode()
 

@@ -108,7 +108,8 @@ sigmoid_attn_varlen_fwd_op.register_autograd(_varlen_backward, setup_context=_va
 
 
 class _VarlenEager(torch.autograd.Function):
-    """Eager-mode path of sigmoid_attention_varlen: the same kernels, saved
+    """Eager-mode path of sigmoid_attention_varlen when the C++ autograd node
+    (_capi.autograd_node) is not used: the same kernels, saved
     tensors and gradients as myops::sigmoid_attn_varlen_fwd with its
     registered autograd, without the custom-op dispatch.  torch.compile
     traces the registered op."""
@@ -226,6 +227,13 @@ def sigmoid_attention_varlen(
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     scale_tensor = _capi.device_constant((), float(scale), torch.float32, query.device)
-    op = sigmoid_attn_varlen_fwd_op if torch.compiler.is_compiling() else _VarlenEager.apply
-    return op(query, key, value, cu_seqlens_k.to(query.device), cu_seqlens_q.to(query.device),
-              int(max_seqlen_k), int(max_seqlen_q), bias, score_mod, scale_tensor, is_causal)
+    cu_seqlens_k, cu_seqlens_q = cu_seqlens_k.to(query.device), cu_seqlens_q.to(query.device)
+    if torch.compiler.is_compiling():
+        return sigmoid_attn_varlen_fwd_op(query, key, value, cu_seqlens_k, cu_seqlens_q, int(max_seqlen_k),
+                                          int(max_seqlen_q), bias, score_mod, scale_tensor, is_causal)
+    node = _capi.autograd_node()
+    if node is not None:
+        return _capi.attention_node_packed(node, query, key, value, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                           max_seqlen_k, bias, score_mod, scale_tensor, is_causal)
+    return _VarlenEager.apply(query, key, value, cu_seqlens_k, cu_seqlens_q, int(max_seqlen_k), int(max_seqlen_q),
+                              bias, score_mod, scale_tensor, is_causal)
