@@ -202,6 +202,33 @@ def test_backward_split_repeats_bitwise_with_score_mod():
         assert_close_to_oracle(a, want, dtype, name)
 
 
+def test_split_at_the_item_count_boundary():
+    """128 items (16 heads x 8 row blocks of 1024 keys) are exactly half of
+    a 256-CU device's CUs: the forward and both backward kernels split in
+    two.  Checked against the unsplit kernels."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("item-count boundaries are stated for a 256-CU device")
+    dtype = torch.float16
+    q, k, v, do = _case(1, 1024, 16, 64, dtype, seed=71)
+    bias, scale = _scalars(1, 1024, 64)
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
+    lib = _capi.load_library()
+    fb = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
+    bb = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
+    assert fb == 512 + 128 * 2 * 128 * 64 * 4
+    assert bb == (512 + 128 * 2 * 128 * 64 * 4) + (512 + 128 * 2 * 2 * 128 * 64 * 4)
+    ref, got = torch.empty_like(q), torch.empty_like(q)
+    _fwd(pr, ref)
+    _fwd(pr, got, _nan_workspace(fb), fb)
+    _assert_fp32_order(got, ref, dtype, "O")
+    ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    got = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd_split(pr, do, *ref)
+    _bwd_split(pr, do, *got, ws=_nan_workspace(bb), nbytes=bb)
+    for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        _assert_fp32_order(a, b, dtype, name)
+
+
 def test_backward_split_halves_equal_the_whole():
     """dQ alone (dk, dv NULL) and dK/dV alone (dq NULL) on the same workspace
     give the whole call's bits."""
@@ -239,11 +266,14 @@ def test_workspace_too_small_is_rejected():
                                  bb - 1, _stream()) == ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("shape", [(4, 1024, 8, 64), (2, 1000, 8, 64), (2, 1024, 8, 64, True)],
-                         ids=["half-full", "short", "causal"])
+@pytest.mark.parametrize("shape", [(4, 1024, 8, 64), (1, 1024, 17, 64), (2, 1000, 8, 64), (2, 1024, 8, 64, True)],
+                         ids=["half-full", "136-items", "short", "causal"])
 def test_grids_that_do_not_split(shape):
-    """256 items already fill half of the GPU; 1000 keys make no two chunks
-    of 512; causal problems never split.  Such problems need no workspace."""
+    """More than half the CUs' worth of items (256; 136 = 17 heads x 8 row
+    blocks) does not split; 1000 keys make no two chunks of 512; causal
+    problems never split.  Such problems need no workspace."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("item-count boundaries are stated for a 256-CU device")
     B, T, H, D = shape[:4]
     causal = len(shape) > 4
     q, k, v, do = _case(B, T, H, D, torch.float16, seed=51)
