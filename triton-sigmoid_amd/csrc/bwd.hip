@@ -19,7 +19,6 @@
 // with the MFMA chains of the next; the dQ kernel (two waves per SIMD) relies
 // on the second wave for that overlap.  Rows past seq_lens are fetched as
 // copies of the last valid row (in bounds) and masked on boundary tiles.
-#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -1263,19 +1262,6 @@ static void bwd_dq_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   });
 }
 
-// Compute units of the current device (cached per device; 0 if unknown).
-static int device_cu_count() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 template <typename T, int D, bool DSOUT>
 static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   launch_rows<128>(kp, kp.Tk, [&](const KParams &p, dim3 grid) {
@@ -1284,7 +1270,8 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
       // one when a non-causal grid of pairs would not fill the GPU.
       if (!(p.ragged() && p.B <= 64)) {
         const int64_t paired = (int64_t)((p.nblk + 1) / 2) * p.B * p.H;
-        grid = dim3((unsigned)(!causal && paired < device_cu_count() ? (int64_t)p.nblk * p.B * p.H : paired));
+        const bool one_block = !causal && paired < device_compute_units();
+        grid = dim3((unsigned)(one_block ? (int64_t)p.nblk * p.B * p.H : paired));
       }
       if (causal) {
         if (sm) bwd_dkdv_pair_kernel<T, true, true, DSOUT><<<grid, 512, 0, st>>>(p);

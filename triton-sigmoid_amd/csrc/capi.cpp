@@ -108,20 +108,6 @@ bool is_ragged(const sigattn_problem *p) {
          p->cu_seqlens_k != nullptr;
 }
 
-// Compute units of the current device (cached per device; 0 if unknown, e.g.
-// without a GPU).
-int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 // Fewest rows of the streamed range (keys for the forward and dQ kernels,
 // queries for dK/dV) that a range-split chunk takes; chunks of at least
 // twice as many may run two workgroups per CU.
@@ -174,8 +160,8 @@ bool splittable(const sigattn_problem *p, bool mfma) {
 RangeSplit fwd_range_split(const sigattn_problem *p, bool mfma) {
   if (!splittable(p, mfma)) return RangeSplit{};
   const int D = (int)p->D, BM = sigattn::fwd_rows_per_workgroup(D);
-  return range_split(p->B * p->H * cdiv(p->Tq, BM), device_cus(), sigattn::fwd_workgroups_per_cu(D), p->Tk,
-                     (int64_t)BM * D);
+  return range_split(p->B * p->H * cdiv(p->Tq, BM), sigattn::device_compute_units(),
+                     sigattn::fwd_workgroups_per_cu(D), p->Tk, (int64_t)BM * D);
 }
 
 // The recompute backward's split: the dQ kernel splits keys, the D = 64
@@ -189,7 +175,7 @@ struct BwdSplit {
 BwdSplit bwd_range_split(const sigattn_problem *p, bool mfma) {
   BwdSplit s;
   if (!splittable(p, mfma) || (p->D != 64 && p->D != 128)) return s;
-  const int D = (int)p->D, cus = device_cus();
+  const int D = (int)p->D, cus = sigattn::device_compute_units();
   const int RQ = sigattn::bwd_dq_rows_per_workgroup(), RK = sigattn::bwd_dkdv_rows_per_workgroup();
   s.dq = range_split(p->B * p->H * cdiv(p->Tq, RQ), cus, sigattn::bwd_dq_workgroups_per_cu(D), p->Tk,
                      (int64_t)RQ * D);
@@ -240,6 +226,20 @@ int launch_status() {
 }
 
 }  // namespace
+
+namespace sigattn {
+int device_compute_units() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+}  // namespace sigattn
 
 extern "C" {
 

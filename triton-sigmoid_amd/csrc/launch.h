@@ -12,6 +12,10 @@ constexpr int kF16 = 0;
 constexpr int kBF16 = 1;
 constexpr int kF32 = 2;
 
+// Compute units of the current device (cached per device; 0 if unknown, e.g.
+// without a GPU).  Defined with the C ABI.
+int device_compute_units();
+
 // Rows per workgroup and resident workgroups per CU of the MFMA forward and
 // of the recompute backward's kernels (D in {64, 128}); the range split of
 // small dense grids (KParams::rsplit) sizes itself from them.
