@@ -5,8 +5,9 @@ and the dK/dV kernel each item's query range, into two to four chunks of at
 least 512 rows, one workgroup each; the
 last workgroup of an item to finish adds the partials in chunk order and
 stores the result (sigattn_fwd_ws / sigattn_bwd_split).  The reference runs
-one program per row block whatever the grid size
-(src/triton_sigmoid/sigmoid_triton_dense.py:99-118, 162-307); the results
+one program per row block, streaming every key, whatever the grid size
+(src/triton_sigmoid/sigmoid_triton_dense.py:108-118 and grid :534; backward
+:162-307); the results
 must match the float64 oracle like the unsplit kernels' and equal them within
 fp32 summation order, and repeated calls must be bitwise equal.
 
