@@ -6,7 +6,7 @@ SIGATTN_EAGER_BINDING=python), so outputs and gradients must be bitwise
 equal to theirs; the Python nodes are checked against the oracle by the
 other GPU tests.  The reference's eager path is the Python autograd of
 src/triton_sigmoid/sigmoid_triton_dense.py:696-753 and
-sigmoid_triton_padded.py:790-880."""
+sigmoid_triton_padded.py:780-846."""
 
 import math
 

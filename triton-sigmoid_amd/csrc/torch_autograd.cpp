@@ -3,7 +3,7 @@
 //
 // The reference builds its eager path from torch.autograd.Function-style
 // registrations in Python (src/triton_sigmoid/sigmoid_triton_dense.py:696-753,
-// sigmoid_triton_padded.py:790-880).  The same node written in Python costs
+// sigmoid_triton_padded.py:780-846).  The same node written in Python costs
 // tens of microseconds of host time per forward+backward before any kernel
 // runs -- more than a small problem's kernels take -- and PyTorch's autograd
 // engine runs a CUDA node's backward on its device thread, where a Python
