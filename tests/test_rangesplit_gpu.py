@@ -251,6 +251,51 @@ def test_backward_split_halves_equal_the_whole():
         assert torch.equal(a, b), f"{name}: half call differs from the whole"
 
 
+def _random_split_cases(n=12, seed=2024):
+    """Seeded shapes that split (B*H*row blocks within half of 256 CUs,
+    T >= 1024), across head dims, dtypes and score_mod."""
+    import random
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        D = rng.choice([64, 128])
+        T = rng.randrange(1024, 3300)
+        H = rng.randrange(1, 5)
+        B = rng.randrange(1, 3)
+        if B * H * -(-T // 128) > 128:  # the backward kernels' 128-row blocks
+            continue
+        cases.append((B, T, H, D, rng.choice([torch.float16, torch.bfloat16]), rng.random() < 0.5))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_split_cases(), ids=lambda c: "B{}T{}H{}D{}{}{}".format(
+    c[0], c[1], c[2], c[3], str(c[4])[6:], "sm" if c[5] else ""))
+def test_random_split_shapes_equal_unsplit(case):
+    """Forward and backward through the split kernels equal the unsplit
+    ones within fp32 summation order on seeded random shapes (ragged last
+    tiles and row blocks, 2-4 chunks)."""
+    B, T, H, D, dtype, with_sm = case
+    print(f"random split case {case}", flush=True)
+    q, k, v, do = _case(B, T, H, D, dtype, seed=T * 7 + H)
+    sm = randn((B, T), torch.float32, DEV, torch.Generator().manual_seed(T), std=2.0) if with_sm else None
+    bias, scale = _scalars(B, T, D)
+    pr = _capi._problem(q, k, v, bias, sm, scale, None, None, False)
+    lib = _capi.load_library()
+    fb = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
+    bb = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
+    assert fb > 0 and bb > 0, "this shape should take the range split"
+    ref, got = torch.empty_like(q), torch.empty_like(q)
+    _fwd(pr, ref)
+    _fwd(pr, got, _nan_workspace(fb), fb)
+    _assert_fp32_order(got, ref, dtype, "O")
+    ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    got = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
+    _bwd_split(pr, do, *ref)
+    _bwd_split(pr, do, *got, ws=_nan_workspace(bb), nbytes=bb)
+    for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        _assert_fp32_order(a, b, dtype, name)
+
+
 def test_workspace_too_small_is_rejected():
     q, k, v, do = _case(1, 1024, 2, 64, torch.float16, seed=31)
     bias, scale = _scalars(1, 1024, 64)
