@@ -26,6 +26,7 @@ bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 KParams make_params(const sigattn_problem *p) {
   KParams k{};
+  k.ncu = sigattn::device_compute_units();
   k.q = p->q;
   k.k = p->k;
   k.v = p->v;

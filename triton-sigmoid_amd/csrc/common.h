@@ -101,6 +101,7 @@ struct KParams {
   int rsplit;
   float *rs_part;
   int *rs_cnt;
+  int ncu;  // compute units of the device (WorkOrder::by_level's dealing rounds)
 
   // Valid query / key rows of batch b.
   __device__ __forceinline__ int len_q(int b) const {
@@ -189,6 +190,14 @@ struct WorkItem {
 #define SIGATTN_STREAM_GROUPED 1
 #endif
 
+// Dealing order of WorkOrder::by_level (see dealt).  Measured on MI355X at
+// fp16 B=8 Lmax=2048 H=8 D=64 causal, seq_lens 682-1789 (three runs each,
+// kernel times in us, plain / 1 / 2): forward 39.2 / 34.9 / 35.8, dQ 51.3 /
+// 52.0 / 51.3, dK/dV 68.1 / 65.5 / 72.3.
+#ifndef SIGATTN_LEVEL_DEAL
+#define SIGATTN_LEVEL_DEAL 1
+#endif
+
 struct WorkOrder {
   // Row blocks of batch `lane` (0 for lanes past B); rows(b) = valid rows.
   template <class Len>
@@ -257,11 +266,29 @@ struct WorkOrder {
     const int p0 = (x - s8 + 8) & 7;
     return base + ((id - start - p0) >> 3);
   }
+  // Position in the heaviest-first order of the item that workgroup `id`
+  // runs, out of n.  The hardware places workgroup ids breadth-first over
+  // the S compute units (ids kS .. kS+S-1 form round k, one per CU, when the
+  // slots are free), so in the plain order every round gives its heaviest
+  // item to the same CUs; dealt in reverse, a round gives the CU that ran a
+  // round's heaviest item its lightest (SIGATTN_LEVEL_DEAL: 0 plain, 1 odd
+  // rounds reversed, 2 every round after the first reversed).
+  static __device__ __forceinline__ int dealt(int id, int n, int S) {
+    if (SIGATTN_LEVEL_DEAL == 0 || S <= 0 || id >= n) return id;
+    const int k = id / S, j = id - k * S, m = min(S, n - k * S);
+    const bool rev = SIGATTN_LEVEL_DEAL == 1 ? (k & 1) != 0 : k > 0;
+    return rev ? k * S + (m - 1 - j) : id;
+  }
   template <class RowLen>
   static __device__ __forceinline__ WorkItem by_level(int id, int B, int H, RowLen rows, int RB, int nlev,
-                                                      bool descending) {
+                                                      bool descending, int ncu = 0) {
     const int lane = __lane_id();
     const int nv = row_blocks(rows, RB, B, lane);
+    if (SIGATTN_LEVEL_DEAL != 0) {
+      int total = 0;
+      for (int k = 0; k < B; ++k) total += __builtin_amdgcn_readlane(nv, k);
+      id = dealt(id, total * H, ncu);
+    }
     int base = 0;
     for (int t = 0; t < nlev; ++t) {
       const int lev = descending ? nlev - 1 - t : t;
