@@ -143,6 +143,42 @@ def test_padded_many_batches_odd_key_blocks(causal):
         assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
 
 
+@pytest.mark.parametrize("D,B,H", [(64, 48, 2), (128, 64, 3)])
+def test_causal_padded_dealing_rounds(D, B, H):
+    """Causal ragged batches deal their items heaviest level first over the
+    GPU's compute units, every odd round of workgroup ids in reverse
+    (WorkOrder::dealt).  These shapes give the forward, dQ and dK/dV kernels
+    about 290-580 valid items: a full first round, a reversed odd round and
+    partial last rounds, with padding items past them.  Every valid row is
+    held to the reference's criterion (fp32 and mixed eager paths, as in
+    test_padded_reference_criterion), and the packed layout, a different
+    caller of the same work order, must match the padded one bit for bit."""
+    T = 400
+    dtype = torch.float16
+    tol = get_tolerance(dtype)
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=1000 + D, std=0.5, noise=False, lo=0.5)
+    q_valid = torch.arange(T)[None, :] < sq.cpu()[:, None]
+    fn = lambda a, b, c: ts.sigmoid_attention_padded(a, b, c, seq_lens_k=sk, seq_lens_q=sq, is_causal=True)
+    errs = criterion_errors(q, k, v, do, fn, dict(seq_lens_k=sk, seq_lens_q=sq, causal=True),
+                            q_valid=q_valid, k_valid=q_valid)
+    assert_reference_criterion(errs, tol)
+
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = fn(*leaves)
+    o.backward(do)
+    lens = sq.cpu().tolist()
+    rows = lambda t: torch.cat([t[b, :lens[b]] for b in range(B)])
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=DEV)
+    pk = [rows(t).detach().clone().requires_grad_(True) for t in (q, k, v)]
+    op = ts.sigmoid_attention_varlen(*pk, cu, cu, max_seqlen_q=T, max_seqlen_k=T, is_causal=True)
+    op.backward(rows(do))
+    assert torch.equal(op, rows(o.detach()))
+    for name, a, b_ in zip(("dQ", "dK", "dV"), pk, leaves):
+        assert torch.equal(a.grad, rows(b_.grad)), name
+    for b in range(B):  # padded key rows get exactly zero gradients
+        assert torch.all(leaves[1].grad[b, lens[b]:] == 0) and torch.all(leaves[2].grad[b, lens[b]:] == 0)
+
+
 # The reference's test_op grid (tests/test_sigmoid_padded.py:48-186): B, H in
 # {(1, 2), (4, 8)}, (Tq, Tk) pairs, D in {64, 128}, causal (skipped for
 # Tq > Tk, as there), fp16 / bf16 / fp32, seq_lens ~ U[0.8 T, T], N(0, 0.5²)
