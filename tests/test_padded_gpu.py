@@ -146,10 +146,12 @@ def test_padded_many_batches_odd_key_blocks(causal):
 @pytest.mark.parametrize("D,B,H", [(64, 48, 2), (128, 64, 3)])
 def test_causal_padded_dealing_rounds(D, B, H):
     """Causal ragged batches deal their items heaviest level first over the
-    GPU's compute units, every odd round of workgroup ids in reverse
-    (WorkOrder::dealt).  These shapes give the forward, dQ and dK/dV kernels
-    about 290-580 valid items: a full first round, a reversed odd round and
-    partial last rounds, with padding items past them.  Every valid row is
+    GPU's compute units, every odd round of workgroup ids placed at launch
+    in reverse (WorkOrder::dealt; D = 64, where a CU holds two or three
+    workgroups; the D = 128 kernels hold one and keep the plain order).
+    These shapes give the kernels about 290-580 valid items: a full first
+    round, a reversed odd round and partial last rounds, with padding items
+    past them.  Every valid row is
     held to the reference's criterion (fp32 and mixed eager paths, as in
     test_padded_reference_criterion), and the packed layout, a different
     caller of the same work order, must match the padded one bit for bit."""

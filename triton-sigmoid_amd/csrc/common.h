@@ -268,26 +268,28 @@ struct WorkOrder {
   }
   // Position in the heaviest-first order of the item that workgroup `id`
   // runs, out of n.  The hardware places workgroup ids breadth-first over
-  // the S compute units (ids kS .. kS+S-1 form round k, one per CU, when the
-  // slots are free), so in the plain order every round gives its heaviest
-  // item to the same CUs; dealt in reverse, a round gives the CU that ran a
+  // the S compute units (ids kS .. kS+S-1 form round k, one per CU, while
+  // the slots are free), so in the plain order every round placed at launch
+  // (the first `occ`, the kernel's workgroups per CU) gives its heaviest item
+  // to the same CUs; dealt in reverse, a round gives the CU that ran a
   // round's heaviest item its lightest (SIGATTN_LEVEL_DEAL: 0 plain, 1 odd
-  // rounds reversed, 2 every round after the first reversed).
-  static __device__ __forceinline__ int dealt(int id, int n, int S) {
+  // rounds reversed, 2 every round after the first reversed).  Later rounds
+  // start as slots free and keep the heaviest-first order.
+  static __device__ __forceinline__ int dealt(int id, int n, int S, int occ) {
     if (SIGATTN_LEVEL_DEAL == 0 || S <= 0 || id >= n) return id;
     const int k = id / S, j = id - k * S, m = min(S, n - k * S);
-    const bool rev = SIGATTN_LEVEL_DEAL == 1 ? (k & 1) != 0 : k > 0;
+    const bool rev = k < occ && (SIGATTN_LEVEL_DEAL == 1 ? (k & 1) != 0 : k > 0);
     return rev ? k * S + (m - 1 - j) : id;
   }
   template <class RowLen>
   static __device__ __forceinline__ WorkItem by_level(int id, int B, int H, RowLen rows, int RB, int nlev,
-                                                      bool descending, int ncu = 0) {
+                                                      bool descending, int ncu = 0, int occ = 1) {
     const int lane = __lane_id();
     const int nv = row_blocks(rows, RB, B, lane);
-    if (SIGATTN_LEVEL_DEAL != 0) {
+    if (SIGATTN_LEVEL_DEAL != 0 && occ > 1) {
       int total = 0;
       for (int k = 0; k < B; ++k) total += __builtin_amdgcn_readlane(nv, k);
-      id = dealt(id, total * H, ncu);
+      id = dealt(id, total * H, ncu, occ);
     }
     int base = 0;
     for (int t = 0; t < nlev; ++t) {
