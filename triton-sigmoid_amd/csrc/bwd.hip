@@ -51,7 +51,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu, 2)
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
+                                                     D == 64 ? 3 : 2)
                                : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb = it.blk;
   } else {
