@@ -755,7 +755,16 @@ def measure_config(name: str, steps: int, warmup: int) -> dict:
         o = attn()
         o.backward(do)
 
-    # Whole-job timing of K fwd+bwd steps.
+    # The per-kernel and forward-only timings run first.  Besides their own
+    # figures they take the GPU through its power-management settling (a
+    # process's first steps run at the cold clock, the next ones throttled),
+    # so the K timed steps below measure the steady state a training loop
+    # runs at rather than the first tens of milliseconds of a process.
+    kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, steps), seq_lens=sl)
+    fwd_ms, _ = time_region(fwd, iters=max(10, steps), warmup=3)
+    fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
+
+    # Whole-job timing of K fwd+bwd steps after W untimed ones.
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -765,10 +774,6 @@ def measure_config(name: str, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / steps
     fb_tflops = fb_flops / (ms_step * 1e-3) / 1e12
-
-    fwd_ms, _ = time_region(fwd, iters=max(10, steps), warmup=3)
-    fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
-    kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, iters=max(10, steps), seq_lens=sl)
     dominant = max(kt, key=kt.get)
     log(f"[bench] config={name} {cfg}")
     log(f"[bench] step {ms_step:.3f} ms -> fwd+bwd {fb_tflops:.1f} TFLOPS ({100 * fb_tflops / PEAK_BF16_TFLOPS:.1f}% peak)")

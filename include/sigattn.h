@@ -129,7 +129,11 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
  * order inside the same launch; sigattn_fwd_workspace_bytes then returns the
  * partials' size (it asks the current device for its compute-unit count, and
  * returns 0 without a device).  Deterministic, and equal to sigattn_fwd
- * within fp32 summation order.
+ * within fp32 summation order.  A workspace too small for these partials (for
+ * instance one sized for split-KV decode) or not 16-byte aligned is not an
+ * error here: the problem then runs unsplit, exactly as in sigattn_fwd.  (A
+ * split-KV problem given a workspace smaller than its partials still returns
+ * SIGATTN_ERR_WORKSPACE.)
  */
 size_t sigattn_fwd_workspace_bytes(const sigattn_problem *p);
 int sigattn_fwd_ws(const sigattn_problem *p, void *out, void *workspace, size_t workspace_bytes,

@@ -75,6 +75,13 @@ int bwd_dkdv_workgroups_per_cu(int D) { return D == 64 ? 2 : 1; }
 void launch_rs_clear(int *, int na, int *, int nb, hipStream_t) {
   if (na + nb > 0) g_calls.emplace_back("rs_clear");
 }
+GapAxis g_gap[2];
+void launch_zero_gaps(const GapAxis &a, const GapAxis &b, int, hipStream_t) {
+  if (a.rows + b.rows > 0) {
+    g_calls.emplace_back("zero_gaps");
+    g_gap[0] = a, g_gap[1] = b;
+  }
+}
 // The fixed scratch of sigattn_fwd_noalloc: any aligned address stands in.
 hipError_t splitkv_scratch(float **ptr) {
   *ptr = reinterpret_cast<float *>(uintptr_t(3) << 20);
@@ -225,6 +232,30 @@ int main() {
     EXPECT(g_calls.empty());
   }
   {
+    // Packed layout: the rows outside every sequence are zeroed by one launch
+    // ahead of the attention kernels, for the outputs each call writes.
+    sigattn_problem p = base(3, 300, 2, 128);
+    p.cu_seqlens_q = p.cu_seqlens_k = (const int32_t *)kFake;
+    p.rows_q = 700, p.rows_k = 650;
+    p.q_stride_b = p.k_stride_b = 0;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "zero_gaps,fwd_mfma");
+    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[0].T == 300 && sigattn::g_gap[0].out[0] == kFake &&
+           sigattn::g_gap[1].rows == 0);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "zero_gaps,dq_mfma,dkdv_mfma");
+    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[1].rows == 650 && sigattn::g_gap[1].B == 3 &&
+           sigattn::g_gap[1].out[0] == kFake && sigattn::g_gap[1].out[1] == kFake);
+    EXPECT(sigattn_bwd_dkdv(&p, kFake, kFake, kFake, nullptr) == 0 && calls() == "zero_gaps,dkdv_mfma");
+    EXPECT(sigattn::g_gap[0].rows == 0 && sigattn::g_gap[1].rows == 650);
+    // No sequences (B = 0) or no queries: every row is a gap; none without rows.
+    p.B = 0;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "zero_gaps");
+    EXPECT(sigattn_fwd(&p, nullptr, nullptr) == SIGATTN_ERR_NULL_ARG);
+    EXPECT(sigattn_bwd(&p, nullptr, kFake, kFake, kFake, nullptr) == 0 && calls() == "zero_gaps");
+    p.rows_q = p.rows_k = 0;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && sigattn_bwd(&p, nullptr, kFake, kFake, kFake, nullptr) == 0);
+    EXPECT(g_calls.empty());
+  }
+  {
     // Range split of small dense non-causal grids, on a device of 256 CUs:
     // B=2 L=1024 H=8 D=64 has 128 workgroups per kernel.
     g_cus = 256;
@@ -234,7 +265,10 @@ int main() {
     EXPECT(fw == 512 + size_t(128) * 2 * 128 * 64 * 4);  // counters, then 2 partials per item
     EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw, nullptr) == 0 && calls() == "rs_clear,fwd_mfma");
     EXPECT(g_last.rsplit == 2 && g_last.rs_cnt == kFake && (char *)g_last.rs_part == (char *)kFake + 512);
-    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw - 1, nullptr) == SIGATTN_ERR_WORKSPACE && g_calls.empty());
+    // A workspace too small for the partials, or misaligned: unsplit, as sigattn_fwd.
+    EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw - 1, nullptr) == 0 && calls() == "fwd_mfma" && g_last.rsplit == 0);
+    EXPECT(sigattn_fwd_ws(&p, kFake, (char *)kFake + 8, fw, nullptr) == 0 && calls() == "fwd_mfma" &&
+           g_last.rsplit == 0);
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_last.rsplit == 0);
     EXPECT(sigattn_fwd_noalloc(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_last.rsplit == 0);
     const size_t bw = sigattn_bwd_split_workspace_bytes(&p);

@@ -179,3 +179,45 @@ def test_cpp_node_workspace_oom_falls_back_to_recompute(monkeypatch):
         torch.cuda.empty_cache()
     for name, x, y in zip(("O", "dQ", "dK", "dV"), got, ref):
         assert torch.equal(x, y), f"{name}: OOM fallback differs from the recompute backward"
+
+
+HOOK_CASES = [  # (B, Tq, Tk, H, D, dtype, causal, padded)
+    (2, 384, 384, 4, 128, torch.bfloat16, True, False),   # two-pass backward
+    (2, 1024, 1024, 8, 64, torch.float16, False, False),  # range-split recompute backward
+    (3, 300, 420, 2, 64, torch.float16, True, True),      # padded
+]
+
+
+@pytest.mark.parametrize("binding", ["cpp", "python"])
+@pytest.mark.parametrize("hook", ["save_on_cpu", "checkpoint"])
+@pytest.mark.parametrize("case", HOOK_CASES, ids=lambda c: f"D{c[4]}{'p' if c[7] else ''}{'c' if c[6] else ''}")
+def test_saved_tensor_hooks_give_plain_gradients(case, hook, binding, monkeypatch):
+    """Under saved-tensor hooks the backward receives new Q / K / V tensors at
+    new addresses, and the forward's buffers (Q, K, V are computed inside the
+    hooked region here) are freed and then overwritten with NaN: the gradients
+    must still equal those of a plain backward bit for bit."""
+    B, Tq, Tk, H, D, dtype, causal, padded = case
+    q, k, v, do = _case(B, Tq, Tk, H, D, dtype, seed=Tq + D)
+    if padded:
+        sq = torch.tensor([Tq, 17, 250], dtype=torch.int32, device=DEV)
+        sk = torch.tensor([Tk, 33, 1], dtype=torch.int32, device=DEV)
+
+    def fn(q, k, v):
+        q, k, v = q * 1.0, k * 1.0, v * 1.0  # fresh buffers, referenced only by the saved tensors
+        if padded:
+            return ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal)
+        return ts.sigmoid_attention(q, k, v, is_causal=causal)
+
+    want, _ = _run(fn, (q, k, v), do, binding, monkeypatch)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+    if hook == "save_on_cpu":
+        with torch.autograd.graph.save_on_cpu():
+            o = fn(*leaves)
+    else:
+        o = torch.utils.checkpoint.checkpoint(fn, *leaves, use_reentrant=False)
+    junk = [torch.full_like(t, float("nan")) for t in (q, k, v, q, k, v)]
+    o.backward(do)
+    torch.cuda.synchronize()
+    del junk
+    for name, x, y in zip(("O", "dQ", "dK", "dV"), [o.detach()] + [t.grad for t in leaves], want):
+        assert torch.equal(x, y), f"{name} under {hook} ({binding} node) differs from the plain backward"

@@ -140,6 +140,35 @@ def test_baseline_configs_within_2e2(cfg):
         assert err <= 2e-2, (name, err)
 
 
+@pytest.mark.parametrize("B,T,H", [(2, 8192, 16), (1, 16384, 16)], ids=["L8192-two-pass", "L16384-recompute"])
+def test_reference_grid_long_shapes_within_2e2(B, T, H):
+    """The long end of the reference's benchmark grid (bf16 D=128 non-causal,
+    sigmoid_bias=0, B = 16384/L, H = 2048/D: benchmarks/benchmark_sigmoid.py:
+    193,202), through the public API.  At L=8192 the backward is the two-pass
+    one in two groups of 8 heads (the 2 GiB workspace cap); at L=16384 a group
+    that fits (4 heads) would not fill the GPU, so the recompute backward runs.
+    Each (batch, head) slice is checked against fp32 eager within 2e-2."""
+    D = 128
+    q, k, v, do = _inputs(B, T, H, D, torch.bfloat16, seed=T)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, sigmoid_bias=0.0)
+    o.backward(do)
+    worst = {}
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(None), slice(h, h + 1))
+            qq, kk, vv = (t[sl].detach().float().requires_grad_(True) for t in (q, k, v))
+            ro = sigmoid_attention_eager(qq, kk, vv, sigmoid_bias=0.0, upcast=True)
+            ro.backward(do[sl].float())
+            for name, got, want in (("O", o[sl], ro), ("dQ", q.grad[sl], qq.grad), ("dK", k.grad[sl], kk.grad),
+                                    ("dV", v.grad[sl], vv.grad)):
+                worst[name] = max(worst.get(name, 0.0), (got.float() - want.detach()).abs().max().item())
+            del ro, qq, kk, vv
+    for name, err in worst.items():
+        assert err <= 2e-2, (name, err)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_c1_fp32_matches_oracle(causal):
     """fp32 B=2 L=256 H=4 D=64, q/k/v/dO ~ N(0,1)

@@ -296,17 +296,26 @@ def test_random_split_shapes_equal_unsplit(case):
         _assert_fp32_order(a, b, dtype, name)
 
 
-def test_workspace_too_small_is_rejected():
+def test_workspace_too_small():
+    """sigattn_fwd_ws with a workspace too small for the range split's
+    partials (say, one sized for split-KV decode), or misaligned, runs the
+    problem unsplit: the result equals sigattn_fwd's bit for bit.
+    sigattn_bwd_split, which asks for the split explicitly, rejects it."""
     q, k, v, do = _case(1, 1024, 2, 64, torch.float16, seed=31)
     bias, scale = _scalars(1, 1024, 64)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()
     fb = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
     bb = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
-    ws = _nan_workspace(max(fb, bb))
-    o = torch.empty_like(q)
-    assert lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), ws.data_ptr(), fb - 1, _stream()) == \
-        ERR_WORKSPACE
+    assert fb > 0 and bb > 0, "this shape should take the range split"
+    ws = _nan_workspace(max(fb, bb) + 16)
+    ref = torch.empty_like(q)
+    assert lib.sigattn_fwd(ctypes.byref(pr), ref.data_ptr(), _stream()) == 0
+    for ptr, nbytes in ((ws.data_ptr(), fb - 1), (ws.data_ptr() + 8, fb)):
+        o = torch.full_like(q, float("nan"))
+        assert lib.sigattn_fwd_ws(ctypes.byref(pr), o.data_ptr(), ptr, nbytes, _stream()) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref)
     g = [torch.empty_like(t) for t in (q, k, v)]
     assert lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), *(t.data_ptr() for t in g), ws.data_ptr(),
                                  bb - 1, _stream()) == ERR_WORKSPACE

@@ -123,29 +123,70 @@ def test_varlen_many_sequences_and_zero_lengths():
                          _run_varlen(q, k, v, do, sq, sk, True), sq, sk, "B=80")
 
 
-@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (32, torch.float32)])
-def test_packed_kernels_write_only_sequence_rows(D, dtype):
-    """Through the C ABI: rows outside every sequence keep their contents
-    (cu_seqlens ends before the last row), and sequences are computed as usual."""
+def _packed_c_abi(q, k, v, do, cu, T, causal, fill):
+    """sigattn_fwd and sigattn_bwd on packed rows through the C ABI, with
+    every output pre-filled with `fill`."""
     lib = _capi.load_library()
-    H, rows = 2, 700
-    g = torch.Generator().manual_seed(9)
-    q, k, v, do = (randn((rows, H, D), dtype, DEV, g) for _ in range(4))
-    cu = torch.tensor([0, 250, 250, 611], dtype=torch.int32, device=DEV)   # rows 611.. are outside
-    bias = -torch.log(torch.tensor([250.0, 0.0, 361.0], device=DEV))   # as the API computes it
-    scale = torch.tensor(1 / math.sqrt(D), dtype=torch.float32, device=DEV)
-    pr = _capi._problem(q, k, v, bias, None, scale, None, None, True, packed=(cu, cu, 361, 361))
-    out, dq, dk, dv = (torch.full_like(q, float("nan")) for _ in range(4))
+    B = cu.numel() - 1
+    lens = (cu[1:] - cu[:-1]).clamp(min=1).float()
+    bias = -torch.log(lens).to(DEV)
+    scale = torch.tensor(1 / math.sqrt(q.shape[-1]), dtype=torch.float32, device=DEV)
+    pr = _capi._problem(q, k, v, bias, None, scale, None, None, causal, packed=(cu, cu, T, T))
+    out, dq, dk, dv = (torch.full_like(q, fill) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     assert lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream) == 0
     assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                            stream) == 0
     torch.cuda.synchronize()
-    for t in (out, dq, dk, dv):
-        assert torch.all(torch.isnan(t[611:]))
-        assert torch.all(torch.isfinite(t[:611]))
-    want = ts.sigmoid_attention_varlen(q[:611], k[:611], v[:611], cu, cu, 361, 361, is_causal=True)
-    assert torch.equal(out[:611], want)
+    assert B >= 0
+    return out, dq, dk, dv
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16), (32, torch.float32)])
+@pytest.mark.parametrize("cu_rows,T,outside", [
+    # non-decreasing cu: rows before cu[0] and past cu[B], and rows 550..610
+    # past the longest sequence T = 300 of the 361-row sequence 2
+    ([40, 250, 250, 611], 300, [(0, 40), (550, 611), (611, 700)]),
+    # decreasing cu (sequence 1 is empty): rows 100..299 and 400.. outside
+    ([300, 400, 0, 100], 100, [(100, 300), (400, 700)]),
+], ids=["sorted", "unsorted"])
+def test_packed_rows_outside_sequences_are_zero(D, dtype, cu_rows, T, outside):
+    """Through the C ABI, outputs pre-filled with NaN: the rows no sequence
+    covers come back as zeros in O, dQ, dK and dV, the rows of the sequences
+    are finite and equal to a run whose outputs started as zeros."""
+    H, rows = 2, 700
+    g = torch.Generator().manual_seed(9)
+    q, k, v, do = (randn((rows, H, D), dtype, DEV, g) for _ in range(4))
+    cu = torch.tensor(cu_rows, dtype=torch.int32, device=DEV)
+    got = _packed_c_abi(q, k, v, do, cu, T, True, float("nan"))
+    ref = _packed_c_abi(q, k, v, do, cu, T, True, 0.0)
+    mask = torch.zeros(rows, dtype=torch.bool, device=DEV)
+    for a, b in outside:
+        mask[a:b] = True
+    for name, t, r in zip(("O", "dQ", "dK", "dV"), got, ref):
+        assert torch.all(t[mask] == 0), f"{name}: rows outside every sequence are not zero"
+        assert torch.all(torch.isfinite(t[~mask])), f"{name}: a sequence row is not finite"
+        assert torch.equal(t, r), f"{name}: differs from the run on zero-filled outputs"
+
+
+def test_packed_api_rows_outside_sequences_are_zero():
+    """The public API (C++ and Python nodes alike go through the C ABI):
+    cu_seqlens covering rows 0..599 of 640, and B = 0 (no sequence at all)."""
+    H, D, rows = 2, 64, 640
+    g = torch.Generator().manual_seed(12)
+    q, k, v, do = (randn((rows, H, D), torch.bfloat16, DEV, g).requires_grad_(True) for _ in range(4))
+    cu = torch.tensor([0, 250, 600], dtype=torch.int32, device=DEV)
+    o = ts.sigmoid_attention_varlen(q, k, v, cu, cu, 350, 350, is_causal=True)
+    o.backward(do.detach())
+    for name, t in (("O", o), ("dQ", q.grad), ("dK", k.grad), ("dV", v.grad)):
+        assert torch.all(t[600:] == 0), name
+        assert torch.all(torch.isfinite(t[:600])), name
+    none = torch.zeros(1, dtype=torch.int32, device=DEV)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+    o = ts.sigmoid_attention_varlen(*leaves, none, none, 0, 0)
+    o.backward(do.detach())
+    for name, t in zip(("O", "dQ", "dK", "dV"), [o] + [t.grad for t in leaves]):
+        assert torch.all(t == 0), f"B = 0: {name} is not all zeros"
 
 
 def test_varlen_empty_batch_and_validation():

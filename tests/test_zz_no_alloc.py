@@ -42,6 +42,35 @@ def _with_workspace(lib, pr, out):
     return nbytes
 
 
+def test_noalloc_first_call_under_graph_capture():
+    """The first sigattn_fwd_noalloc call of the process on this device comes
+    while torch.cuda.graph captures (so the scratch address is looked up under
+    capture), on a split-KV shape; every replay, with eager work and
+    synchronisation between replays and the output overwritten with NaN first,
+    equals the eager sigattn_fwd_ws result bit for bit.  It runs first in
+    this file, whose tests are the only callers of sigattn_fwd_noalloc."""
+    lib = _capi.load_library()
+    q, k, v, sq, sk, bias, scale, pr = _case(2, 4, 8192, 8, 128, torch.bfloat16, seed=99, lens_k=[8192, 3000])
+    want = torch.empty_like(q)
+    assert _with_workspace(lib, pr, want) > 0  # the problem splits
+    torch.cuda.synchronize()
+    got = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.sigattn_fwd_noalloc(ctypes.byref(pr), got.data_ptr(), side.cuda_stream)
+    assert rc == 0, _capi.strerror(rc)
+    for rep in range(3):
+        busy = (q.float() * 2.0).sum()
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(busy)
+        assert torch.equal(got, want), f"replay {rep} differs from sigattn_fwd_ws"
+
+
 def test_noalloc_matches_workspace_entry_point_on_two_calls():
     lib = _capi.load_library()
     stream = torch.cuda.current_stream().cuda_stream

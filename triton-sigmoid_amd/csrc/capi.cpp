@@ -222,6 +222,29 @@ KParams head_slice(const KParams &k, int64_t h0, int64_t nh, int64_t esize) {
   return s;
 }
 
+// Packed layout: zeros on the rows of the outputs that no sequence covers
+// (rows before cu_seqlens[0], past cu_seqlens[B], past the longest sequence
+// Tq / Tk of a longer one), so every row of a packed output is written.
+// q_out is the Q-shaped output (O or dQ), k_out0 / k_out1 the K-shaped ones
+// (dK, dV); nullptr skips a tensor.  One launch for both axes, on `st`.
+void zero_packed_gaps(const sigattn_problem *p, void *q_out, void *k_out0, void *k_out1, hipStream_t st) {
+  if (p->H == 0) return;
+  sigattn::GapAxis a, b;
+  if (p->cu_seqlens_q != nullptr && q_out != nullptr && p->rows_q > 0) {
+    a.cu = p->cu_seqlens_q;
+    a.B = (int)p->B, a.T = (int)p->Tq, a.H = (int)p->H, a.D = (int)p->D;
+    a.rows = p->rows_q, a.st = p->q_stride_t, a.sh = p->q_stride_h;
+    a.out[0] = q_out;
+  }
+  if (p->cu_seqlens_k != nullptr && (k_out0 != nullptr || k_out1 != nullptr) && p->rows_k > 0) {
+    b.cu = p->cu_seqlens_k;
+    b.B = (int)p->B, b.T = (int)p->Tk, b.H = (int)p->H, b.D = (int)p->D;
+    b.rows = p->rows_k, b.st = p->k_stride_t, b.sh = p->k_stride_h;
+    b.out[0] = k_out0, b.out[1] = k_out1;
+  }
+  sigattn::launch_zero_gaps(a, b, p->dtype == SIGATTN_F32 ? 4 : 2, st);
+}
+
 int launch_status() {
   return hipGetLastError() == hipSuccess ? SIGATTN_OK : SIGATTN_ERR_LAUNCH;
 }
@@ -319,11 +342,19 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
                     bool static_scratch, void *stream) {
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
-  if (p->B == 0 || p->H == 0 || p->Tq == 0) return SIGATTN_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  if (p->B == 0 || p->H == 0 || p->Tq == 0) {
+    // Packed rows without any sequence (no batches, or no queries) are all
+    // written as zeros.
+    if (p->cu_seqlens_q == nullptr || p->H == 0 || p->rows_q == 0) return SIGATTN_OK;
+    if (out == nullptr) return SIGATTN_ERR_NULL_ARG;
+    (void)hipGetLastError();
+    zero_packed_gaps(p, out, nullptr, nullptr, st);
+    return launch_status();
+  }
   if (out == nullptr) return SIGATTN_ERR_NULL_ARG;
   KParams k = make_params(p);
   k.out = out;
-  const hipStream_t st = (hipStream_t)stream;
   const void *ptrs[4] = {p->q, p->k, p->v, out};
   const bool mfma = use_mfma(p, ptrs, 4);
   SplitPlan sp = splitkv_plan(p, mfma);
@@ -340,12 +371,16 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     sp.nsplit = 1;  // no workspace: one chunk per (batch, head), written directly
     sp.chunk = (int)(cdiv(p->Tk, 128) * 128);
   }
+  // The range split is an optimisation the caller need not know about: a
+  // workspace that cannot hold its partials (one sized for split-KV decode,
+  // say) or that is misaligned runs the problem unsplit, as sigattn_fwd does.
   RangeSplit rs;
   if (sp.nsplit == 0 && workspace != nullptr && !static_scratch) {
     rs = fwd_range_split(p, mfma);
-    if (rs.n > 1 && ((size_t)rs.bytes > workspace_bytes || !aligned16(workspace))) return SIGATTN_ERR_WORKSPACE;
+    if (rs.n > 1 && ((size_t)rs.bytes > workspace_bytes || !aligned16(workspace))) rs = RangeSplit{};
   }
   (void)hipGetLastError();
+  zero_packed_gaps(p, out, nullptr, nullptr, st);
   if (rs.n > 1) {
     use_range_split(k, rs, workspace);
     sigattn::launch_rs_clear(k.rs_cnt, (int)rs.items, nullptr, 0, st);
@@ -383,7 +418,18 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   const int rc = sigattn_check(p);
   if (rc != SIGATTN_OK) return rc;
   if (workspace != nullptr && !aligned16(workspace)) return SIGATTN_ERR_WORKSPACE;
-  if (p->B == 0 || p->H == 0) return SIGATTN_OK;
+  if (p->H == 0) return SIGATTN_OK;
+  if (p->B == 0) {
+    // Packed rows without any sequence are all written as zeros.
+    const bool rows_q = p->cu_seqlens_q != nullptr && p->rows_q > 0;
+    const bool rows_k = p->cu_seqlens_k != nullptr && p->rows_k > 0;
+    if (!rows_q && !rows_k) return SIGATTN_OK;
+    void *zq = parts != kBwdDkdv ? dq : nullptr;
+    void *zk = parts != kBwdDq ? dk : nullptr, *zv = parts != kBwdDq ? dv : nullptr;
+    (void)hipGetLastError();
+    zero_packed_gaps(p, zq, zk, zv, (hipStream_t)stream);
+    return launch_status();
+  }
   const bool need_dq = parts != kBwdDkdv && p->Tq > 0;
   const bool need_dkdv = parts != kBwdDq && p->Tk > 0;
   const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
@@ -418,6 +464,8 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
   const int dt = p->dtype, D = (int)p->D;
   (void)hipGetLastError();
+  zero_packed_gaps(p, parts != kBwdDkdv ? dq : nullptr, parts != kBwdDq ? dk : nullptr,
+                   parts != kBwdDq ? dv : nullptr, st);
   if (twopass) {
     k.ds = (uint16_t *)workspace;
     k.ds_nqb = (int)cdiv(p->Tq, 32);

@@ -53,8 +53,17 @@ hipError_t splitkv_scratch(float **ptr) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     p = g_scratch[dev].load(std::memory_order_relaxed);
     if (p == nullptr) {
+      // The first call may come while this thread captures a graph in the
+      // global mode, which refuses runtime calls it deems unsafe; the lookup
+      // enqueues nothing, so it runs in the relaxed mode, and the thread's
+      // mode is restored afterwards.
+      hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+      e = hipThreadExchangeStreamCaptureMode(&mode);
+      if (e != hipSuccess) return e;
       void *addr = nullptr;
       e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      const hipError_t restore = hipThreadExchangeStreamCaptureMode(&mode);
+      if (e == hipSuccess) e = restore;
       if (e != hipSuccess) return e;
       if (addr == nullptr) return hipErrorInvalidSymbol;
       p = static_cast<float *>(addr);

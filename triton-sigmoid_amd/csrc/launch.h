@@ -56,6 +56,19 @@ constexpr size_t kSplitScratchBytes = size_t(16) << 20;
 // device with hipGetSymbolAddress); hipSuccess or the lookup's error.
 hipError_t splitkv_scratch(float **ptr);
 
+// One packed sequence axis for launch_zero_gaps: cu_seqlens [B + 1], the
+// axis's row count, its longest sequence T, the outputs' row and head strides
+// (elements) and up to two output tensors (nullptr: none).
+struct GapAxis {
+  const int32_t *cu = nullptr;
+  int B = 0, T = 0, H = 0, D = 0;
+  int64_t rows = 0, st = 0, sh = 0;
+  void *out[2] = {nullptr, nullptr};
+};
+// Zeroes the rows of packed outputs that no sequence covers, for two axes in
+// one launch (an axis with rows = 0 takes no workgroups); esize = 2 or 4.
+void launch_zero_gaps(const GapAxis &a, const GapAxis &b, int esize, hipStream_t st);
+
 // Portable kernels: any dtype, D in {16, 32, 64, 128}, any alignment.
 void launch_fwd_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
 void launch_bwd_dq_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);

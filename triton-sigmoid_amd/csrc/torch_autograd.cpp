@@ -180,8 +180,10 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
     ctx->saved_data["bwd_limit"] = bwd_limit;
     ctx->saved_data["max_seqlen_q"] = max_seqlen_q;
     ctx->saved_data["max_seqlen_k"] = max_seqlen_k;
+    // Packed rows with no sequence at all (B = 0) are zeros.
+    if (lay.packed() && lay.cuq.numel() == 1) return at::zeros_like(q);
     Tensor out = at::empty_like(q);
-    if (out.numel() == 0 || (lay.packed() && lay.cuq.numel() == 1)) return out;
+    if (out.numel() == 0) return out;
     const c10::DeviceGuard guard(q.device());
     const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, lay, causal);
     const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
@@ -204,10 +206,13 @@ struct SigattnNode : public torch::autograd::Function<SigattnNode> {
     if (dout.scalar_type() != q.scalar_type() || dout.device() != q.device() || !dout.is_contiguous())
       dout = dout.to(q.device(), q.scalar_type()).contiguous();
     TORCH_CHECK(dout.sizes() == q.sizes(), "dO shape ", dout.sizes(), " != Q shape ", q.sizes());
-    Tensor dq = at::empty_like(q), dk = at::empty_like(k), dv = at::empty_like(v);
+    const bool no_seqs = lay.packed() && lay.cuq.numel() == 1;  // B = 0: every packed row is outside
+    Tensor dq = no_seqs ? at::zeros_like(q) : at::empty_like(q);
+    Tensor dk = no_seqs ? at::zeros_like(k) : at::empty_like(k);
+    Tensor dv = no_seqs ? at::zeros_like(v) : at::empty_like(v);
     tensor_list result(14);
     result[0] = dq, result[1] = dk, result[2] = dv;  // none for bias, score_mod, ... (no gradient)
-    if ((dq.numel() == 0 && dk.numel() == 0) || (lay.packed() && lay.cuq.numel() == 1)) return result;
+    if ((dq.numel() == 0 && dk.numel() == 0) || no_seqs) return result;
     const c10::DeviceGuard guard(q.device());
     const int dev = q.device().index();
     const sigattn_problem p = make_problem(q, k, v, bias, sm, scale, lay, causal);

@@ -404,11 +404,23 @@ def forward_eager(Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, ca
     return out, (pr if all(a is b for a, b in zip(given, canon)) else None)
 
 
+def _problem_points_at(pr: SigattnProblem, Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k) -> bool:
+    """True when every pointer of `pr` is the address of the matching tensor.
+    Saved-tensor hooks (torch.autograd.graph.save_on_cpu, non-reentrant
+    checkpointing) hand the backward new tensors at new addresses, and the
+    forward's buffers may since have been freed and reused."""
+    pairs = ((pr.q, Q), (pr.k, K), (pr.v, V), (pr.bias, bias), (pr.scale, sm_scale), (pr.score_mod, score_mod),
+             (pr.seq_lens_q, seq_lens_q), (pr.seq_lens_k, seq_lens_k))
+    return all((p or None) == _ptr(t) for p, t in pairs) and all(
+        t is None or t.is_contiguous() for t in (Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k))
+
+
 def backward_eager(pr, Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal):
-    """backward() on the problem forward_eager returned for the same saved
-    tensors (which keep every pointer in it alive), or backward() itself
-    when there is none."""
-    if pr is None:
+    """backward() on the problem forward_eager returned, when that problem
+    still points at exactly the saved tensors given here (which then keep
+    every pointer in it alive); backward() itself otherwise -- no problem, or
+    saved tensors that a saved-tensor hook moved."""
+    if pr is None or not _problem_points_at(pr, Q, K, V, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k):
         return backward(Q, K, V, dO, bias, score_mod, sm_scale, seq_lens_q, seq_lens_k, causal)
     lib = load_library()
     dO = _as(dO, Q.dtype, Q.device)
@@ -461,8 +473,10 @@ def forward_packed(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
     lib = load_library()
     Q, K, V, bias, score_mod, sm_scale, _, _ = _prepare(Q, K, V, bias, score_mod, sm_scale, None, None)
     cu_q, cu_k = _prepare_packed(cu_seqlens_q, cu_seqlens_k, Q.device)
+    if cu_q.numel() == 1:
+        return torch.zeros_like(Q)  # no sequences: every packed row is outside them
     out = torch.empty_like(Q)
-    if out.numel() == 0 or cu_q.numel() == 1:
+    if out.numel() == 0:
         return out
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
                   packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))
@@ -479,8 +493,10 @@ def backward_packed(Q, K, V, dO, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_s
     dO = _as(dO, Q.dtype, Q.device)
     if dO.shape != Q.shape:
         raise RuntimeError(f"dO shape {tuple(dO.shape)} != Q shape {tuple(Q.shape)}")
+    if cu_q.numel() == 1:
+        return torch.zeros_like(Q), torch.zeros_like(K), torch.zeros_like(V)
     dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
-    if (dQ.numel() == 0 and dK.numel() == 0) or cu_q.numel() == 1:
+    if dQ.numel() == 0 and dK.numel() == 0:
         return dQ, dK, dV
     pr = _problem(Q, K, V, bias, score_mod, sm_scale, None, None, causal,
                   packed=_packed_dims(Q, K, cu_q, cu_k, max_seqlen_q, max_seqlen_k))

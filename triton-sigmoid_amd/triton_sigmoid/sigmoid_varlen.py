@@ -178,11 +178,10 @@ def sigmoid_attention_varlen(
         [total_q, H, D] output, equal row for row to what
         `sigmoid_attention_padded` returns for the same sequences.
 
-    Rows outside every sequence are never written, in the output or in the
-    gradients: rows past cu[B] when cu does not cover all rows, and rows past
-    max_seqlen of a longer sequence, hold whatever the freshly allocated
-    tensors held (uninitialised memory).  Callers that pass such rows must
-    ignore those rows of dQ / dK / dV, or make cu_seqlens cover every row.
+    Rows outside every sequence -- before cu[0], past cu[B] when cu does not
+    cover all rows, and past max_seqlen of a longer sequence -- are zeros in
+    the output and in dQ / dK / dV (they take no part in the attention), so
+    no gradient row is left uninitialised.
     """
     if query.dim() != 3 or key.dim() != 3 or value.dim() != 3:
         raise ValueError("Expected query, key, and value to be 3D tensors (total_tokens, H, D)")
