@@ -141,32 +141,44 @@ def test_baseline_configs_within_2e2(cfg):
 
 
 @pytest.mark.parametrize("B,T,H", [(2, 8192, 16), (1, 16384, 16)], ids=["L8192-two-pass", "L16384-recompute"])
-def test_reference_grid_long_shapes_within_2e2(B, T, H):
+def test_reference_grid_long_shapes(B, T, H):
     """The long end of the reference's benchmark grid (bf16 D=128 non-causal,
     sigmoid_bias=0, B = 16384/L, H = 2048/D: benchmarks/benchmark_sigmoid.py:
     193,202), through the public API.  At L=8192 the backward is the two-pass
     one in two groups of 8 heads (the 2 GiB workspace cap); at L=16384 a group
     that fits (4 heads) would not fill the GPU, so the recompute backward runs.
-    Each (batch, head) slice is checked against fp32 eager within 2e-2."""
-    D = 128
+
+    With sigmoid_bias=0 every P is near 1/2 and O sums thousands of them:
+    |O| reaches ~150 and one bf16 rounding step there is 1.0, so an absolute
+    2e-2 bound cannot hold for any bf16 kernel.  Each (batch, head) slice is
+    held instead to the reference tests' relative criterion against fp32 eager
+    (error <= 2x (forward) / 3x (backward) the mixed-precision eager path's
+    error + tol, tests/test_sigmoid_dense.py:111-114,154-166) and to 2e-2 of
+    the slice's largest fp32 magnitude."""
+    from oracle.eager import mixed_fwd_bwd
+    D, tol = 128, get_tolerance(torch.bfloat16)
     q, k, v, do = _inputs(B, T, H, D, torch.bfloat16, seed=T)
     for t in (q, k, v):
         t.requires_grad_(True)
     o = ts.sigmoid_attention(q, k, v, sigmoid_bias=0.0)
     o.backward(do)
-    worst = {}
+    ours = (o.detach(), q.grad, k.grad, v.grad)
     for b in range(B):
         for h in range(H):
             sl = (slice(b, b + 1), slice(None), slice(h, h + 1))
             qq, kk, vv = (t[sl].detach().float().requires_grad_(True) for t in (q, k, v))
             ro = sigmoid_attention_eager(qq, kk, vv, sigmoid_bias=0.0, upcast=True)
             ro.backward(do[sl].float())
-            for name, got, want in (("O", o[sl], ro), ("dQ", q.grad[sl], qq.grad), ("dK", k.grad[sl], kk.grad),
-                                    ("dV", v.grad[sl], vv.grad)):
-                worst[name] = max(worst.get(name, 0.0), (got.float() - want.detach()).abs().max().item())
-            del ro, qq, kk, vv
-    for name, err in worst.items():
-        assert err <= 2e-2, (name, err)
+            ref = (ro.detach(), qq.grad, kk.grad, vv.grad)
+            mixed = mixed_fwd_bwd(*(t[sl].detach() for t in (q, k, v, do)), sigmoid_bias=0.0)
+            for i, name in enumerate(("O", "dQ", "dK", "dV")):
+                r = ref[i].float()
+                err = (ours[i][sl].float() - r).abs().max().item()
+                err_mixed = (mixed[i].float() - r).abs().max().item()
+                f = 2.0 if name == "O" else 3.0
+                assert err <= f * err_mixed + tol, (b, h, name, err, err_mixed)
+                assert err <= 2e-2 * r.abs().max().item(), (b, h, name, err, r.abs().max().item())
+            del ro, qq, kk, vv, ref, mixed
 
 
 @pytest.mark.parametrize("causal", [False, True])
