@@ -84,8 +84,9 @@ typedef struct sigattn_problem {
    * sequence b is rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1, clamped to
    * [0, rows_q] and to at most Tq rows (Tq = the longest sequence), and
    * seq_lens_q must be NULL.  Likewise cu_seqlens_k / rows_k / Tk for K, V,
-   * dK, dV; score_mod is then packed [rows_k].  Outputs are written on the
-   * rows of the sequences only.
+   * dK, dV; score_mod is then packed [rows_k].  Every row of a packed output
+   * is written: rows that no sequence covers (before cu_seqlens[0], past
+   * cu_seqlens[B], past Tq / Tk rows of a longer sequence) get zeros.
    */
   const int32_t *cu_seqlens_q; /* [B+1] int32 or NULL */
   const int32_t *cu_seqlens_k; /* [B+1] int32 or NULL */
@@ -103,7 +104,7 @@ int sigattn_check(const sigattn_problem *p);
 
 /*
  * Forward: out[B, Tq, H, D] (q strides).  Rows at or past seq_lens_q[b] are
- * written as zeros (packed layout: only the sequences' rows are written).
+ * written as zeros (packed layout: rows outside every sequence are zeros).
  * `stream` is a hipStream_t (NULL = default stream).
  */
 int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
@@ -123,10 +124,12 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
  * Range split of small dense grids (no counterpart in the reference): a
  * dense non-causal problem taking the MFMA kernels whose workgroups (one per
  * 128 or 256 queries of every (batch, head)) would leave at least half of
- * the GPU's compute units idle, and whose keys number at least 1024, runs
- * each query block's keys as 2-4 chunks of at least 512 keys in as many
- * workgroups, whose fp32 partials the last one to finish adds in chunk
- * order inside the same launch; sigattn_fwd_workspace_bytes then returns the
+ * the GPU's compute units idle, runs each query block's keys as 2-4 chunks
+ * of at least 512 keys in as many workgroups when the chunks save at least
+ * 1024 keys of each block's range at head_dim 64 (512 at head_dim 128; so
+ * T >= 1536 and T >= 1024), whose fp32 partials the last one to finish adds
+ * in chunk order inside the same launch (an agent-scope acquire-release
+ * counter orders the hand-over); sigattn_fwd_workspace_bytes then returns the
  * partials' size (it asks the current device for its compute-unit count, and
  * returns 0 without a device).  Deterministic, and equal to sigattn_fwd
  * within fp32 summation order.  A workspace too small for these partials (for
@@ -172,7 +175,8 @@ int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
  * 64 or 128 taking the MFMA kernels, whose dQ or dK/dV grid would leave at
  * least half of the GPU's compute units idle, the dQ kernel runs each query
  * block's keys and (head_dim 64) the dK/dV kernel each key block's queries
- * as 2-4 chunks of at least 512 rows (so T >= 1024), the fp32
+ * as 2-4 chunks of at least 512 rows, saving at least 1024 rows of each
+ * range at head_dim 64 and 512 at 128 (so T >= 1536 and T >= 1024), the fp32
  * partials added in chunk order by the last chunk to finish, inside the
  * same launch.  sigattn_bwd_split_workspace_bytes(p) is the workspace it
  * needs (0 when nothing splits, or without a device); with workspace NULL

@@ -257,10 +257,11 @@ int main() {
   }
   {
     // Range split of small dense non-causal grids, on a device of 256 CUs:
-    // B=2 L=1024 H=8 D=64 has 128 workgroups per kernel.
+    // B=1 L=2048 H=8 D=64 has 128 workgroups per kernel.
     g_cus = 256;
-    sigattn_problem p = base(2, 1024, 8, 64);
-    // 128 items of 1024 keys: two chunks of 512 keys, one workgroup per CU.
+    sigattn_problem p = base(1, 2048, 8, 64);
+    // 128 items of 2048 keys: two chunks of 1024 keys (saving 1024 rows per
+    // item), one workgroup per CU.
     const size_t fw = sigattn_fwd_workspace_bytes(&p);
     EXPECT(fw == 512 + size_t(128) * 2 * 128 * 64 * 4);  // counters, then 2 partials per item
     EXPECT(sigattn_fwd_ws(&p, kFake, kFake, fw, nullptr) == 0 && calls() == "rs_clear,fwd_mfma");
@@ -305,8 +306,16 @@ int main() {
            calls() == "rs_clear,dq_mfma,dkdv_mfma" && g_last.rsplit == 0);
     c = base(4, 1024, 8, 64);  // 256 items: the GPU is already half full
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
-    c = base(2, 1000, 8, 64);  // keys too few for two chunks of 512
+    // At D = 64 a split must save 1024 rows per item: c2 (B=2 L=1024 H=8) in two
+    // chunks saves 512; 2000 keys save 1000 in two, and three chunks of 128
+    // items exceed one workgroup per CU.
+    c = base(2, 1024, 8, 64);
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    c = base(1, 2000, 8, 64);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 0 && sigattn_bwd_split_workspace_bytes(&c) == 0);
+    // Three chunks of 1536 keys (saving 1024 rows) for 24 items.
+    c = base(1, 1536, 2, 64);
+    EXPECT(sigattn_fwd_workspace_bytes(&c) == 256 + size_t(24) * 3 * 128 * 64 * 4);
     // Four chunks at 2048 keys per item of 64 items (one workgroup per CU),
     // and at 4096 keys per item of 128 items (chunks of 1024: two per CU).
     c = base(1, 2048, 4, 64);

@@ -52,7 +52,8 @@ def _assert_same(cpp, py, what):
 
 
 DENSE = [  # (B, T, H, D, dtype, causal)
-    (2, 1024, 8, 64, torch.float16, False),   # c2: range split forward and backward
+    (2, 1024, 8, 64, torch.float16, False),   # c2: too few keys for the range split
+    (1, 2048, 4, 64, torch.float16, False),   # range split forward and backward
     (2, 1024, 8, 64, torch.float16, True),
     (2, 384, 4, 128, torch.bfloat16, False),  # two-pass backward
     (1, 2048, 2, 128, torch.bfloat16, False), # range split forward and dQ
@@ -183,7 +184,7 @@ def test_cpp_node_workspace_oom_falls_back_to_recompute(monkeypatch):
 
 HOOK_CASES = [  # (B, Tq, Tk, H, D, dtype, causal, padded)
     (2, 384, 384, 4, 128, torch.bfloat16, True, False),   # two-pass backward
-    (2, 1024, 1024, 8, 64, torch.float16, False, False),  # range-split recompute backward
+    (1, 2048, 2048, 4, 64, torch.float16, False, False),  # range-split recompute backward
     (3, 300, 420, 2, 64, torch.float16, True, True),      # padded
 ]
 

@@ -264,6 +264,22 @@ def test_device_code_has_no_packed_fp32_instructions(src):
     asm = subprocess.run(cmd, capture_output=True, text=True, check=True).stdout
     assert "v_mfma" in asm or src == "generic.hip"
     assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)
+    # The range split's arrival counter (split_combine) is an agent-scope
+    # acquire-release atomic: in every kernel that counts, the add sits
+    # between the release (L2 write-back) and the acquire (L2 invalidate),
+    # and the partials move with agent-coherent (sc1) accesses.
+    atomics = 0
+    for body in re.split(r"\n(?=_Z\w+:)", asm):
+        lines = [ln.strip() for ln in body.splitlines()]
+        adds = [i for i, ln in enumerate(lines) if ln.startswith("global_atomic_add ")]
+        for i in adds:
+            atomics += 1
+            assert any(ln.startswith("buffer_wbl2 sc1") for ln in lines[max(0, i - 4):i]), "no release before the add"
+            assert any(ln.startswith("buffer_inv sc1") for ln in lines[i + 1:i + 5]), "no acquire after the add"
+        if adds:
+            assert any(ln.startswith("buffer_store_dwordx4") and ln.endswith("sc1") for ln in lines)
+            assert any(ln.startswith("buffer_load_dwordx4") and ln.endswith("sc1") for ln in lines)
+    assert (atomics > 0) == (src in ("fwd.hip", "bwd.hip"))
 
 
 def test_backward_workspace_oom_falls_back_to_recompute(monkeypatch):

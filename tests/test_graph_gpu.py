@@ -24,7 +24,7 @@ def _case(kind):
     if kind == "dense_d64_range_split":
         # A small dense non-causal grid: forward, dQ and dK/dV range-split,
         # their arrival counters cleared by a captured kernel each replay.
-        B, T, H, D, dtype = 1, 1100, 2, 64, torch.float16
+        B, T, H, D, dtype = 1, 2100, 2, 64, torch.float16
         q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
         return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v)
     B, T, H, D, dtype = 3, 200, 2, 64, torch.float16

@@ -2,7 +2,8 @@
 problem's (batch, head, row block) items leave at least half of the GPU's
 compute units idle, the forward and dQ kernels split each item's key range,
 and the dK/dV kernel each item's query range, into two to four chunks of at
-least 512 rows, one workgroup each; the
+least 512 rows, one workgroup each, when the split saves at least 1024 rows
+of an item's range at head_dim 64 (512 at head_dim 128); the
 last workgroup of an item to finish adds the partials in chunk order and
 stores the result (sigattn_fwd_ws / sigattn_bwd_split).  The reference runs
 one program per row block, streaming every key, whatever the grid size
@@ -77,10 +78,10 @@ def _assert_fp32_order(got, ref, dtype, name):
 
 
 # (B, T, H, D): every shape splits on a 256-CU device (dense problems have
-# Tq = Tk), in two chunks (T = 1024, 1100), three (T = 1700) or four
-# (T = 2100).  T = 1100, 1700 and 2100 leave a ragged last key tile in the
+# Tq = Tk), in two chunks (T = 1024 at D = 128), three (T = 1536, 1700) or
+# four (T = 2100).  T = 1700 and 2100 leave a ragged last key tile in the
 # last chunk and a ragged last row block.
-FWD_SHAPES = [(1, 1024, 2, 64), (2, 1100, 2, 64), (1, 2100, 2, 64), (1, 1024, 2, 128), (1, 1700, 1, 128)]
+FWD_SHAPES = [(1, 1536, 2, 64), (2, 1700, 2, 64), (1, 2100, 2, 64), (1, 1024, 2, 128), (1, 1700, 1, 128)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -106,7 +107,7 @@ def test_forward_split_matches_oracle_and_unsplit(shape, dtype):
 def test_forward_split_with_score_mod():
     """score_mod is indexed by the absolute key: each chunk offsets it by its
     first key."""
-    B, T, H, D, dtype = 2, 1024, 2, 64, torch.bfloat16
+    B, T, H, D, dtype = 2, 1536, 2, 64, torch.bfloat16
     q, k, v, do = _case(B, T, H, D, dtype, seed=5)
     g = torch.Generator().manual_seed(6)
     sm = randn((B, T), torch.float32, DEV, g, std=2.0)
@@ -130,8 +131,8 @@ def test_forward_split_repeats_bitwise_and_reuses_its_workspace():
     them is still right."""
     dtype = torch.float16
     lib = _capi.load_library()
-    q, k, v, do = _case(2, 1024, 4, 64, dtype, seed=11)
-    bias, scale = _scalars(2, 1024, 64)
+    q, k, v, do = _case(1, 2048, 4, 64, dtype, seed=11)
+    bias, scale = _scalars(1, 2048, 64)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     nbytes = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
     assert nbytes > 0
@@ -140,8 +141,8 @@ def test_forward_split_repeats_bitwise_and_reuses_its_workspace():
     _fwd(pr, a, ws, nbytes)
     _fwd(pr, b, ws, nbytes)
     assert torch.equal(a, b)
-    q2, k2, v2, do2 = _case(1, 1500, 2, 64, dtype, seed=12)
-    bias2, scale2 = _scalars(1, 1500, 64)
+    q2, k2, v2, do2 = _case(1, 1700, 2, 64, dtype, seed=12)
+    bias2, scale2 = _scalars(1, 1700, 64)
     pr2 = _capi._problem(q2, k2, v2, bias2, None, scale2, None, None, False)
     n2 = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr2)))
     assert 0 < n2 <= nbytes
@@ -153,7 +154,7 @@ def test_forward_split_repeats_bitwise_and_reuses_its_workspace():
 
 # (B, T, H, D): at D = 64 the dQ and dK/dV kernels split, at D = 128 the dQ
 # kernel (the dK/dV kernel runs one key block per workgroup).
-BWD_SHAPES = [(1, 1024, 2, 64), (2, 1100, 2, 64), (1, 1700, 1, 64), (1, 2100, 1, 64), (1, 1100, 2, 128),
+BWD_SHAPES = [(1, 1536, 2, 64), (2, 1700, 2, 64), (1, 1700, 1, 64), (1, 2100, 1, 64), (1, 1100, 2, 128),
               (1, 2100, 1, 128)]
 
 
@@ -180,7 +181,7 @@ def test_backward_split_matches_oracle_and_unsplit(shape, dtype):
 
 
 def test_backward_split_repeats_bitwise_with_score_mod():
-    B, T, H, D, dtype = 2, 1024, 2, 64, torch.float16
+    B, T, H, D, dtype = 2, 1536, 2, 64, torch.float16
     q, k, v, do = _case(B, T, H, D, dtype, seed=21)
     g = torch.Generator().manual_seed(22)
     sm = randn((B, T), torch.float32, DEV, g, std=2.0)
@@ -204,14 +205,14 @@ def test_backward_split_repeats_bitwise_with_score_mod():
 
 
 def test_split_at_the_item_count_boundary():
-    """128 items (16 heads x 8 row blocks of 1024 keys) are exactly half of
+    """128 items (8 heads x 16 row blocks of 2048 keys) are exactly half of
     a 256-CU device's CUs: the forward and both backward kernels split in
     two.  Checked against the unsplit kernels."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("item-count boundaries are stated for a 256-CU device")
     dtype = torch.float16
-    q, k, v, do = _case(1, 1024, 16, 64, dtype, seed=71)
-    bias, scale = _scalars(1, 1024, 64)
+    q, k, v, do = _case(1, 2048, 8, 64, dtype, seed=71)
+    bias, scale = _scalars(1, 2048, 64)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()
     fb = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
@@ -233,8 +234,8 @@ def test_split_at_the_item_count_boundary():
 def test_backward_split_halves_equal_the_whole():
     """dQ alone (dk, dv NULL) and dK/dV alone (dq NULL) on the same workspace
     give the whole call's bits."""
-    q, k, v, do = _case(2, 1100, 2, 64, torch.bfloat16, seed=61)
-    bias, scale = _scalars(2, 1100, 64)
+    q, k, v, do = _case(2, 1700, 2, 64, torch.bfloat16, seed=61)
+    bias, scale = _scalars(2, 1700, 64)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()
     nbytes = int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr)))
@@ -253,13 +254,14 @@ def test_backward_split_halves_equal_the_whole():
 
 def _random_split_cases(n=12, seed=2024):
     """Seeded shapes that split (B*H*row blocks within half of 256 CUs,
-    T >= 1024), across head dims, dtypes and score_mod."""
+    T >= 2048 at D = 64 and T >= 1024 at D = 128, so two chunks save enough
+    rows), across head dims, dtypes and score_mod."""
     import random
     rng = random.Random(seed)
     cases = []
     while len(cases) < n:
         D = rng.choice([64, 128])
-        T = rng.randrange(1024, 3300)
+        T = rng.randrange(2048 if D == 64 else 1024, 3300)
         H = rng.randrange(1, 5)
         B = rng.randrange(1, 3)
         if B * H * -(-T // 128) > 128:  # the backward kernels' 128-row blocks
@@ -301,8 +303,8 @@ def test_workspace_too_small():
     partials (say, one sized for split-KV decode), or misaligned, runs the
     problem unsplit: the result equals sigattn_fwd's bit for bit.
     sigattn_bwd_split, which asks for the split explicitly, rejects it."""
-    q, k, v, do = _case(1, 1024, 2, 64, torch.float16, seed=31)
-    bias, scale = _scalars(1, 1024, 64)
+    q, k, v, do = _case(1, 1536, 2, 64, torch.float16, seed=31)
+    bias, scale = _scalars(1, 1536, 64)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()
     fb = int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)))
@@ -321,11 +323,14 @@ def test_workspace_too_small():
                                  bb - 1, _stream()) == ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("shape", [(4, 1024, 8, 64), (1, 1024, 17, 64), (2, 1000, 8, 64), (2, 1024, 8, 64, True)],
-                         ids=["half-full", "136-items", "short", "causal"])
+@pytest.mark.parametrize("shape", [(4, 1024, 8, 64), (1, 2048, 9, 64), (2, 1024, 8, 64), (1, 1400, 4, 64),
+                                   (2, 2048, 8, 64, True)],
+                         ids=["half-full", "144-items", "c2", "short", "causal"])
 def test_grids_that_do_not_split(shape):
-    """More than half the CUs' worth of items (256; 136 = 17 heads x 8 row
-    blocks) does not split; 1000 keys make no two chunks of 512; causal
+    """More than half the CUs' worth of items (256; 144 = 9 heads x 16 row
+    blocks) does not split; at head_dim 64 a split must save 1024 rows of an
+    item's range, which 1024 keys in two chunks (c2) or
+    1400 keys in two do not (and 1400 make no three chunks of 512); causal
     problems never split.  Such problems need no workspace."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("item-count boundaries are stated for a 256-CU device")
@@ -340,13 +345,15 @@ def test_grids_that_do_not_split(shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_public_api_c2_shape(dtype):
-    """The public API at B=2 L=1024 H=8 D=64 non-causal (a benchmark
-    configuration small enough to split) equals the unsplit C-ABI calls
-    within fp32 summation order; the split kernels themselves are pinned to
-    the oracle above."""
+@pytest.mark.parametrize("B,T,H,split", [(2, 1024, 8, False), (1, 2048, 8, True)], ids=["c2", "split"])
+def test_public_api_small_grids(B, T, H, split, dtype):
+    """The public API at B=2 L=1024 H=8 D=64 non-causal (
+    whose keys are too few for a split to pay) equals the unsplit C-ABI calls
+    bit for bit; at B=1 L=2048 H=8 it takes the split and equals the unsplit
+    calls within fp32 summation order (the split kernels themselves are
+    pinned to the oracle above)."""
     import triton_sigmoid as ts
-    B, T, H, D = 2, 1024, 8, 64
+    D = 64
     q, k, v, do = _case(B, T, H, D, dtype, seed=41)
     leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
     o = ts.sigmoid_attention(*leaves)
@@ -354,12 +361,14 @@ def test_public_api_c2_shape(dtype):
     bias, scale = _scalars(B, T, D)
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     lib = _capi.load_library()
-    assert int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr))) > 0
-    assert int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr))) > 0
+    assert (int(lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr))) > 0) == split
+    assert (int(lib.sigattn_bwd_split_workspace_bytes(ctypes.byref(pr))) > 0) == split
     ref_o = torch.empty_like(q)
     _fwd(pr, ref_o)
     ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(k)]
     _bwd_split(pr, do, *ref)
-    _assert_fp32_order(o.detach(), ref_o, dtype, "O")
-    for name, t, r in zip(("dQ", "dK", "dV"), leaves, ref):
-        _assert_fp32_order(t.grad, r, dtype, name)
+    for name, got, want in zip(("O", "dQ", "dK", "dV"), [o.detach()] + [t.grad for t in leaves], [ref_o] + ref):
+        if split:
+            _assert_fp32_order(got, want, dtype, name)
+        else:
+            assert torch.equal(got, want), f"{name}: the unsplit public API differs from the C ABI"

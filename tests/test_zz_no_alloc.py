@@ -101,8 +101,8 @@ def test_noalloc_runs_range_split_problems_unsplit():
     lib = _capi.load_library()
     stream = torch.cuda.current_stream().cuda_stream
     g = torch.Generator().manual_seed(9)
-    q, k, v = (torch.randn((1, 1024, 2, 64), generator=g).to("cuda", torch.float16) for _ in range(3))
-    bias = torch.full((1,), -math.log(1024), dtype=torch.float32, device="cuda")
+    q, k, v = (torch.randn((1, 1536, 2, 64), generator=g).to("cuda", torch.float16) for _ in range(3))
+    bias = torch.full((1,), -math.log(1536), dtype=torch.float32, device="cuda")
     scale = torch.full((), 0.125, dtype=torch.float32, device="cuda")
     pr = _capi._problem(q, k, v, bias, None, scale, None, None, False)
     assert lib.sigattn_fwd_workspace_bytes(ctypes.byref(pr)) > 0

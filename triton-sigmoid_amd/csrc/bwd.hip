@@ -885,6 +885,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
       }
 
+#ifdef SIGATTN_PAIR_AGPR
+      asm volatile("" ::"a"(dva[0][0]));
+#endif
       if (my_k < kmax) {
         uint16_t *vr = (uint16_t *)p.dv + koff + (int64_t)my_k * p.sk_t;
 #pragma unroll
@@ -1002,6 +1005,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
       }
 
+#ifdef SIGATTN_PAIR_AGPR
+      asm volatile("" ::"a"(dka[0][0]));
+#endif
       if (my_k < kmax) {
         uint16_t *kr = (uint16_t *)p.dk + koff + (int64_t)my_k * p.sk_t;
 #pragma unroll

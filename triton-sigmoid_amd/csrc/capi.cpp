@@ -110,37 +110,52 @@ bool is_ragged(const sigattn_problem *p) {
 }
 
 // Fewest rows of the streamed range (keys for the forward and dQ kernels,
-// queries for dK/dV) that a range-split chunk takes; chunks of at least
-// twice as many may run two workgroups per CU.
+// queries for dK/dV) that a range-split chunk takes; chunks of at least twice
+// as many may run two workgroups per CU.
 #ifndef SIGATTN_RS_MIN_ROWS
 #define SIGATTN_RS_MIN_ROWS 512
 #endif
+// Fewest rows an item's split must save (rows - rows / n, the part of its
+// range its slowest chunk no longer streams), by head dim: a split pays only
+// when those rows outweigh its hand-over (the partial stores, the release /
+// acquire around the arrival counter, the partial loads).  Measured on MI355X
+// (fp16 D = 64 / bf16 D = 128 non-causal, us, split vs unsplit): D = 64 saving
+// 512 rows lost (B=2 L=1024 H=8, two chunks: forward 19.6 vs 16.2, backward
+// 49.6 vs 46.8) and saving 1536 gained (B=1 L=2048 H=4, four chunks: forward
+// 22.5 vs 26.4, backward 52.5 vs 80.6); at D = 128, with twice the work per
+// row, saving 512 rows gains (B=1 L=1024 H=8: forward 27.0 vs 30.3, backward
+// 60.6 vs 68.5).
+#ifndef SIGATTN_RS_MIN_SAVED_D64
+#define SIGATTN_RS_MIN_SAVED_D64 1024
+#endif
+#ifndef SIGATTN_RS_MIN_SAVED_D128
+#define SIGATTN_RS_MIN_SAVED_D128 512
+#endif
+int64_t rs_min_saved(int64_t D) { return D == 64 ? SIGATTN_RS_MIN_SAVED_D64 : SIGATTN_RS_MIN_SAVED_D128; }
 
 // Range split of a small dense non-causal grid (KParams::rsplit).  A kernel
 // whose `items` workgroups leave at least half of the GPU's CUs idle runs
 // each item as n chunks of its streamed range of `rows`: the most chunks,
 // up to kRangeSplitMax, that keep every chunk at least SIGATTN_RS_MIN_ROWS
-// long and the grid within one workgroup per CU (two when chunks are at
-// least twice that long, and never more than the kernel's `per_cu_max`
-// resident workgroups).  Measured on MI355X (256 CUs), D = 64 fp16
-// non-causal, GPU time per forward+backward: B=2 L=1024 H=8 62.6 -> 59.2 us
-// (n = 2; n = 4 took 72.9), B=1 L=2048 H=8 107.9 -> 82.1 us (n = 2; n = 4
-// took 90.5), B=1 L=4096 H=4 198.6 -> 134.2 us (n = 4), B=1 L=16384 H=1
-// 759 -> 395 us (n = 4); grids filling half the GPU or more measured slower
-// split (B=4 L=1024 H=8 65.8 -> 80.7 us at n = 2).  Each chunk's partial is
-// `part_floats` fp32 per item, and each item has an int counter: the
-// workspace holds the counters first (256-byte aligned), then the partials.
+// long, save at least `min_saved` rows per item, and keep the grid within
+// one workgroup per CU (two when chunks are at least twice that long, and
+// never more than the kernel's `per_cu_max` resident workgroups).  Grids
+// filling half the GPU or more measured slower split (B=4 L=1024 H=8 D=64:
+// 65.8 -> 80.7 us at n = 2).  Each chunk's partial is `part_floats` fp32 per
+// item, and each item has an int counter: the workspace holds the counters
+// first (256-byte aligned), then the partials.
 struct RangeSplit {
   int n = 1;
   int64_t items = 0, part_floats = 0, cnt_bytes = 0, bytes = 0;
 };
 
-RangeSplit range_split(int64_t items, int64_t cus, int64_t per_cu_max, int64_t rows, int64_t part_floats) {
+RangeSplit range_split(int64_t items, int64_t cus, int64_t per_cu_max, int64_t rows, int64_t part_floats,
+                       int64_t min_saved) {
   RangeSplit r;
   if (items <= 0 || cus <= 0 || 2 * items > cus) return r;
   int64_t n = sigattn::kRangeSplitMax;
   for (; n >= 2; --n) {
-    if (rows < n * SIGATTN_RS_MIN_ROWS) continue;
+    if (rows < n * SIGATTN_RS_MIN_ROWS || rows - rows / n < min_saved) continue;
     int64_t per_cu = rows >= 2 * n * SIGATTN_RS_MIN_ROWS ? 2 : 1;
     if (per_cu > per_cu_max) per_cu = per_cu_max;
     if (n * items <= cus * per_cu) break;
@@ -162,7 +177,7 @@ RangeSplit fwd_range_split(const sigattn_problem *p, bool mfma) {
   if (!splittable(p, mfma)) return RangeSplit{};
   const int D = (int)p->D, BM = sigattn::fwd_rows_per_workgroup(D);
   return range_split(p->B * p->H * cdiv(p->Tq, BM), sigattn::device_compute_units(),
-                     sigattn::fwd_workgroups_per_cu(D), p->Tk, (int64_t)BM * D);
+                     sigattn::fwd_workgroups_per_cu(D), p->Tk, (int64_t)BM * D, rs_min_saved(D));
 }
 
 // The recompute backward's split: the dQ kernel splits keys, the D = 64
@@ -179,10 +194,10 @@ BwdSplit bwd_range_split(const sigattn_problem *p, bool mfma) {
   const int D = (int)p->D, cus = sigattn::device_compute_units();
   const int RQ = sigattn::bwd_dq_rows_per_workgroup(), RK = sigattn::bwd_dkdv_rows_per_workgroup();
   s.dq = range_split(p->B * p->H * cdiv(p->Tq, RQ), cus, sigattn::bwd_dq_workgroups_per_cu(D), p->Tk,
-                     (int64_t)RQ * D);
+                     (int64_t)RQ * D, rs_min_saved(D));
   if (D == 64)
     s.kv = range_split(p->B * p->H * cdiv(p->Tk, RK), cus, sigattn::bwd_dkdv_workgroups_per_cu(D), p->Tq,
-                       2 * (int64_t)RK * D);
+                       2 * (int64_t)RK * D, rs_min_saved(D));
   s.bytes = s.dq.bytes + s.kv.bytes;
   return s;
 }

@@ -597,7 +597,10 @@ constexpr int kBufferWord3 = 0x00020000;
 // for data the writing kernel never reads back (measured: the dS stream of
 // the two-pass backward costs the dK/dV kernel 0.10 ms at the headline shape
 // with it, 0.16 ms without).
-constexpr int kStoreNT = 2;
+#ifndef SIGATTN_DS_STORE_NT
+#define SIGATTN_DS_STORE_NT 1
+#endif
+constexpr int kStoreNT = SIGATTN_DS_STORE_NT ? 2 : 0;
 
 // Chunk c of n of a range of nt tiles: tiles [c*nt/n, (c+1)*nt/n).
 // (c < n <= 8 and nt < 2^26, so 32-bit arithmetic; wave-uniform, kept in an
@@ -613,15 +616,27 @@ constexpr int kRangeSplitMax = 4;
 // accumulators -- NACC f32x16 per lane, acc(i) -- become the item's final
 // sum, or the workgroup learns that another chunk will write the output.
 // Every chunk stores its accumulators to its slot of the item's partials
-// (lane-major, 1 KB per store instruction) and, once the stores have
-// completed, counts itself in; the workgroup whose count completes the item
-// adds all n partials in chunk order, its own from registers, so the sum
-// does not depend on which chunk finishes last.  The partials move through
-// agent-coherent (sc1) buffer accesses around a relaxed agent-scope counter:
-// an agent-scope fence instead would write back and invalidate the whole L2
-// of the XCD, evicting the tiles other workgroups stream.  The other chunks'
-// partials are loaded two accumulators at a time with every chunk's loads in
-// flight together (one memory round trip per pair, not one per chunk).
+// (lane-major, 1 KB per store instruction) and, once the workgroup's stores
+// have completed, counts itself in; the workgroup whose count completes the
+// item adds all n partials in chunk order, its own from registers, so the sum
+// does not depend on which chunk finishes last.  The other chunks' partials
+// are loaded two accumulators at a time with every chunk's loads in flight
+// together (one memory round trip per pair, not one per chunk).
+//
+// Ordering follows the HIP (HSA) memory model at agent scope, because the
+// chunks of an item may run on different XCDs, each with its own L2: the
+// counter is an acquire-release agent-scope atomic, so every chunk's partial
+// stores (made workgroup-visible by __syncthreads before thread 0's release)
+// happen before the last chunk's loads (after its acquire and a second
+// __syncthreads).  On gfx950 the compiler lowers that release to buffer_wbl2
+// sc1 + s_waitcnt vmcnt(0) and the acquire to buffer_inv sc1.  The partials
+// themselves move with agent-coherent (sc1) buffer accesses -- the lowering
+// of agent-scope relaxed atomic stores and loads -- which write through past
+// the L2 and so leave the release's L2 write-back little to do: measured at
+// B=2 L=1024 H=8 D=64 (forward / backward, us), relaxed counter with sc1
+// accesses 17.4 / 43.7, this protocol 19.6 / 49.6, plain accesses with the
+// acquire-release counter 22.4 / 61.0.  (A full agent-scope fence,
+// __threadfence, made a split forward 2.3x slower.)
 // Returns false when this workgroup should exit without writing.
 template <int NACC, int NW, class Acc>
 __device__ __forceinline__ bool split_combine(Acc &&acc, float *part_item, int *cnt, int chunk, int n, int w,
@@ -645,7 +660,7 @@ __device__ __forceinline__ bool split_combine(Acc &&acc, float *part_item, int *
   __shared__ int arrived;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (arrived != n - 1) return false;
   asm volatile("" ::: "memory");

@@ -77,7 +77,11 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
   // score_mod, 8 with it (16 would spill there); measured 2-3 % (8 vs 4) and
   // another 1-2.5 % (16 vs 8) at the headline shapes.  D = 64: 4 (three waves
   // per SIMD, 168 registers each).
+#ifdef SIGATTN_FWD_LA128
+  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : SIGATTN_FWD_LA128) : 4;
+#else
   constexpr int LA = D == 128 ? (SCOREMOD ? 8 : 16) : 4;
+#endif
   constexpr int NWD = 8 * NCB;          // packed P words per block
   constexpr int BAR = NSTEP - LA;       // step of the tile barrier in odd regions
   static_assert(NSTEP % LA == 0, "region shape");
@@ -417,6 +421,11 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
       }
     }
 
+#ifdef SIGATTN_FWD_AGPR
+    // Any AGPR operand makes the compiler select the MFMA form whose
+    // accumulators (srcC / vdst) live in AGPRs.
+    asm volatile("" ::"a"(acc[0][0][0]));
+#endif
     if (!CAUSAL && p.rsplit > 1 &&
         !split_combine<NCB * NDB, NWV>([&](int i) SIGATTN_INLINE -> f32x16 & { return acc[i / NDB][i % NDB]; },
                                        p.rs_part + (int64_t)ritem * p.rsplit * (BM * D), p.rs_cnt + ritem,
