@@ -208,8 +208,8 @@ int sigattn_bwd_dkdv(const sigattn_problem *p, const void *dout, void *dk, void 
  * workspace holds 2 bytes per (query, key) pair of every 32x32 block that has
  * a visible pair (causal: the lower triangle), per batch and head:
  * sigattn_bwd_workspace_bytes(p) for the whole problem, or 0 when the
- * problem takes the portable kernels (fp32, D < 64, misaligned rows), which
- * have no two-pass form.  sigattn_bwd_ws with a smaller workspace runs the
+ * problem has no two-pass form (fp32, D other than 64 or 128, misaligned
+ * rows).  sigattn_bwd_ws with a smaller workspace runs the
  * heads in groups that fit, one group after another on `stream`; with room
  * for less than one head, or workspace NULL, it runs sigattn_bwd.  Results
  * equal sigattn_bwd's within fp32 summation order; the workspace must be

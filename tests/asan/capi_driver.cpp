@@ -184,8 +184,13 @@ int main() {
     EXPECT(g_calls.empty());
   }
   {
-    // fp32, D = 32, misaligned strides: the portable kernels.
+    // D = 32 in bf16: the MFMA kernels, recompute backward (no two-pass workspace).
     sigattn_problem p = base(1, 40, 1, 32);
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma");
+    EXPECT(sigattn_bwd_workspace_bytes(&p) == 0);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    // fp32, D = 16, misaligned strides: the portable kernels.
+    p.D = 16;
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");
     p.D = 64;
     p.dtype = SIGATTN_F32;

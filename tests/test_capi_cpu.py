@@ -179,7 +179,9 @@ def test_decode_workspace_size_and_errors():
 def test_two_pass_backward_workspace_size_and_errors():
     """Two-pass backward: 2 KB per 32x32 (query, key) block per batch and
     head, causal problems keeping the lower triangle only; 0 for problems the
-    portable kernels take.  Bad workspaces are rejected before any launch."""
+    two-pass kernels do not take (fp32, head_dim other than 64 or 128,
+    misaligned strides, empty grids).  Bad workspaces are rejected before any
+    launch."""
     lib = _capi.load_library()
     D, T = 128, 100  # 4 blocks of 32 rows per axis
     p = _problem(B=3, H=5, Tq=T, Tk=T, D=D, q_stride_b=T * 5 * D, q_stride_t=5 * D, q_stride_h=D,

@@ -73,7 +73,7 @@ def _assert_equal_packed(padded, packed, sq, sk, what):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("D", [16, 64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
 @pytest.mark.parametrize("Tq,Tk", [(128, 128), (513, 513), (200, 77), (77, 300)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_varlen_equals_padded_bitwise(dtype, D, Tq, Tk, causal):
@@ -142,7 +142,8 @@ def _packed_c_abi(q, k, v, do, cu, T, causal, fill):
     return out, dq, dk, dv
 
 
-@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16), (32, torch.float32)])
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16), (32, torch.bfloat16),
+                                     (32, torch.float32)])
 @pytest.mark.parametrize("cu_rows,T,outside", [
     # non-decreasing cu: rows before cu[0] and past cu[B], and rows 550..610
     # past the longest sequence T = 300 of the 361-row sequence 2

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
-                                                     D == 64 ? 3 : 2)
+                                                     D <= 64 ? 3 : 2)
                                : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb = it.blk;
   } else {
@@ -257,13 +257,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 // words of the few blocks that need them.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD, bool DSOUT>
-__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
+__global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
   constexpr int BN = 128;                 // keys per workgroup (32 per wave)
   constexpr int BMQ = 64;                 // queries per LDS tile (two 32-query blocks)
   constexpr int NST = 4;                  // LDS ring stages
   constexpr int NKS = D / 16, NDB = D / 32;
   constexpr int NM = 2 * NKS + 4 * NDB;   // MFMAs per region
-  constexpr int LA = D == 64 ? 4 : 8;     // operand read-ahead, in MFMAs
+  constexpr int LA = D <= 64 ? 4 : 8;     // operand read-ahead, in MFMAs
   constexpr int NWIN = NM / 4;            // VALU windows (four MFMAs each) per region
   constexpr int PPW = 8 / NWIN;           // element pairs per window
   constexpr int BAR = NM - LA;            // MFMA position of the tile barrier in odd regions
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lk, BN, p.nblk, false, p.ncu,
-                                                     D == 64 ? 2 : 1)
+                                                     D <= 64 ? 2 : 1)
                                : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lk, BN, p.nblk, lq);
     b = it.b, h = it.h, kblk = it.blk;
   } else {
@@ -885,9 +885,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
       }
 
-#ifdef SIGATTN_PAIR_AGPR
-      asm volatile("" ::"a"(dva[0][0]));
-#endif
       if (my_k < kmax) {
         uint16_t *vr = (uint16_t *)p.dv + koff + (int64_t)my_k * p.sk_t;
 #pragma unroll
@@ -1005,9 +1002,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
         if (r0 + 7 < NB + 2) region(r0 + 7, std::integral_constant<int, 7>{});
       }
 
-#ifdef SIGATTN_PAIR_AGPR
-      asm volatile("" ::"a"(dka[0][0]));
-#endif
       if (my_k < kmax) {
         uint16_t *kr = (uint16_t *)p.dk + koff + (int64_t)my_k * p.sk_t;
 #pragma unroll
@@ -1332,24 +1326,26 @@ static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
   });
 }
 
-// dtype in {kF16, kBF16}, D in {64, 128}.
-template <class F>
+// dtype in {kF16, kBF16}, D in {32, 64, 128} (the two-pass backward's
+// dQ-from-dS kernel: 64 and 128 only).
+template <bool WITH32 = true, class F>
 static void by_type(int dtype, int D, F &&f) {
-  if (dtype == kBF16) {
-    if (D == 128) f((__bf16 *)nullptr, std::integral_constant<int, 128>{});
-    else f((__bf16 *)nullptr, std::integral_constant<int, 64>{});
-  } else {
-    if (D == 128) f((_Float16 *)nullptr, std::integral_constant<int, 128>{});
-    else f((_Float16 *)nullptr, std::integral_constant<int, 64>{});
-  }
+  const auto d = [&](auto *t) {
+    if (D == 128) f(t, std::integral_constant<int, 128>{});
+    else if (!WITH32 || D == 64) f(t, std::integral_constant<int, 64>{});
+    else if constexpr (WITH32) f(t, std::integral_constant<int, 32>{});
+  };
+  if (dtype == kBF16) d((__bf16 *)nullptr);
+  else d((_Float16 *)nullptr);
 }
 
 int bwd_dq_rows_per_workgroup() { return 128; }
 int bwd_dkdv_rows_per_workgroup() { return 128; }
 // Resident workgroups per CU of the recompute kernels at D = 64 (dQ: 32 KB of
-// LDS and at most 168 VGPRs; dK/dV: 64 KB and 128 + 128 registers).
-int bwd_dq_workgroups_per_cu(int D) { return D == 64 ? 3 : 2; }
-int bwd_dkdv_workgroups_per_cu(int D) { return D == 64 ? 2 : 1; }
+// LDS and at most 168 VGPRs; dK/dV: 64 KB and 128 + 128 registers); D = 32
+// the same.
+int bwd_dq_workgroups_per_cu(int D) { return D <= 64 ? 3 : 2; }
+int bwd_dkdv_workgroups_per_cu(int D) { return D <= 64 ? 2 : 1; }
 
 void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool sm, hipStream_t st) {
   by_type(dtype, D, [&](auto *t, auto d) {
@@ -1367,7 +1363,7 @@ void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool 
 }
 
 void launch_bwd_dq_ds_mfma(const KParams &p, int dtype, int D, bool causal, hipStream_t st) {
-  by_type(dtype, D, [&](auto *t, auto d) {
+  by_type<false>(dtype, D, [&](auto *t, auto d) {
     bwd_dq_ds_t<std::remove_pointer_t<decltype(t)>, decltype(d)::value>(p, causal, st);
   });
 }

@@ -57,13 +57,13 @@ bool rows_fit_2g(int64_t T, int64_t stride) {
   return stride == 0 || T <= (((int64_t)1 << 30) - 1) / stride;
 }
 
-// True when the MFMA kernels can take the problem: 16-bit elements, D of 64
-// or 128, every row start 16-byte aligned, and every row of a sequence within
-// 2^31 bytes of the sequence's first row (the tile copies address rows with a
-// 32-bit byte offset from that row).
+// True when the MFMA kernels can take the problem: 16-bit elements, D of 32,
+// 64 or 128, every row start 16-byte aligned, and every row of a sequence
+// within 2^31 bytes of the sequence's first row (the tile copies address rows
+// with a 32-bit byte offset from that row).
 bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
   if (p->dtype == SIGATTN_F32) return false;
-  if (p->D != 64 && p->D != 128) return false;
+  if (p->D != 32 && p->D != 64 && p->D != 128) return false;
   if (!rows_fit_2g(p->Tq, p->q_stride_t) || !rows_fit_2g(p->Tk, p->k_stride_t)) return false;
   const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
                               p->k_stride_b, p->k_stride_t, p->k_stride_h};
@@ -88,9 +88,13 @@ struct SplitPlan {
 #define SIGATTN_SPLIT_TARGET 512
 #endif
 
+// The split-KV kernel and the two-pass backward exist at D = 64 and 128; at
+// D = 32 the main forward and the recompute backward serve every shape.
+bool wide_head(const sigattn_problem *p) { return p->D == 64 || p->D == 128; }
+
 SplitPlan splitkv_plan(const sigattn_problem *p, bool mfma) {
   SplitPlan sp;
-  if (!mfma || p->causal != 0 || p->Tq > 32 || p->Tk < 256 || p->B * p->H == 0) return sp;
+  if (!mfma || !wide_head(p) || p->causal != 0 || p->Tq > 32 || p->Tk < 256 || p->B * p->H == 0) return sp;
   const int64_t want = cdiv(SIGATTN_SPLIT_TARGET, p->B * p->H);
   const int64_t most = cdiv(p->Tk, 256);
   const int64_t n = want < most ? want : most;
@@ -170,7 +174,7 @@ RangeSplit range_split(int64_t items, int64_t cus, int64_t per_cu_max, int64_t r
 }
 
 bool splittable(const sigattn_problem *p, bool mfma) {
-  return mfma && p->causal == 0 && !is_ragged(p) && p->Tq > 0 && p->Tk > 0 && p->B * p->H > 0;
+  return mfma && wide_head(p) && p->causal == 0 && !is_ragged(p) && p->Tq > 0 && p->Tk > 0 && p->B * p->H > 0;
 }
 
 RangeSplit fwd_range_split(const sigattn_problem *p, bool mfma) {
@@ -454,12 +458,12 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   // The halves (kBwdDq, kBwdDkdv) need the whole problem's dS at once: the
   // dQ half reads what a dK/dV half with the same workspace stored.
   int64_t heads_per_pass = 0;
-  if (workspace != nullptr && mfma && p->Tq > 0 && p->Tk > 0) {
+  if (workspace != nullptr && mfma && wide_head(p) && p->Tq > 0 && p->Tk > 0) {
     heads_per_pass = (int64_t)workspace_bytes / ds_bytes_per_head(p);
     if (heads_per_pass > p->H) heads_per_pass = p->H;
   }
   if (parts != kBwdAll && workspace != nullptr) {
-    if (!mfma) return SIGATTN_ERR_WORKSPACE;  // no two-pass kernels for this problem
+    if (!mfma || !wide_head(p)) return SIGATTN_ERR_WORKSPACE;  // no two-pass kernels for this problem
     if (p->Tq > 0 && p->Tk > 0 && heads_per_pass < p->H) return SIGATTN_ERR_WORKSPACE;
   }
   const bool twopass = heads_per_pass > 0;
@@ -514,7 +518,7 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
 size_t sigattn_bwd_workspace_bytes(const sigattn_problem *p) {
   if (sigattn_check(p) != SIGATTN_OK || p->B == 0 || p->H == 0 || p->Tq == 0 || p->Tk == 0) return 0;
   const void *none[1] = {nullptr};
-  if (!use_mfma(p, none, 0)) return 0;
+  if (!use_mfma(p, none, 0) || !wide_head(p)) return 0;
   return (size_t)(ds_bytes_per_head(p) * p->H);
 }
 

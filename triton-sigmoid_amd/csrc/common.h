@@ -471,10 +471,13 @@ __device__ __forceinline__ float acc_read(float v) {
 // SQ_LDS_BANK_CONFLICT): 16-byte operand reads of 32 consecutive rows, the
 // 4-row x 32-column ds_read_b64_tr_b16 groups, and chunk-major 16-byte stores.
 // D = 64 (8 chunks per row, two rows per 64-bank line) uses
-// swz(r) = 4*((r>>1)&1) + ((r>>2)&3).
+// swz(r) = 4*((r>>1)&1) + ((r>>2)&3), and D = 32 (4 chunks per row, four
+// rows per line) swz(r) = (r>>2)&3: in each case any 16 consecutive rows read
+// at one logical chunk land on 16 distinct 16-byte slots of a line.
 template <int D> __device__ __forceinline__ int swz(int row) {
   if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
-  else return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+  else if constexpr (D == 64) return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+  else return (row >> 2) & 3;
 }
 // Element offset of (row, col) in a swizzled tile.
 template <int D> __device__ __forceinline__ int toff(int row, int col) {
@@ -597,10 +600,7 @@ constexpr int kBufferWord3 = 0x00020000;
 // for data the writing kernel never reads back (measured: the dS stream of
 // the two-pass backward costs the dK/dV kernel 0.10 ms at the headline shape
 // with it, 0.16 ms without).
-#ifndef SIGATTN_DS_STORE_NT
-#define SIGATTN_DS_STORE_NT 1
-#endif
-constexpr int kStoreNT = SIGATTN_DS_STORE_NT ? 2 : 0;
+constexpr int kStoreNT = 2;
 
 // Chunk c of n of a range of nt tiles: tiles [c*nt/n, (c+1)*nt/n).
 // (c < n <= 8 and nt < 2^26, so 32-bit arithmetic; wave-uniform, kept in an

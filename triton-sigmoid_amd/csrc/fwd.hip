@@ -33,7 +33,7 @@
 namespace sigattn {
 
 // LDS ring stages of the D = 64 forward: three (48 KB) let three workgroups
-// share a CU, four (64 KB) two.
+// share a CU, four (64 KB) two.  D = 32 keeps four (32 KB).
 #ifndef SIGATTN_FWD_D64_STAGES
 #define SIGATTN_FWD_D64_STAGES 3
 #endif
@@ -60,7 +60,11 @@ constexpr bool kFwdCausalPairs = SIGATTN_FWD_CAUSAL_PAIRS != 0;
 #define SIGATTN_FWD_BH_GROUP 16
 #endif
 constexpr int kFwdBhGroup = SIGATTN_FWD_BH_GROUP;
-template <int D> constexpr int fwd_occupancy() { return D == 64 ? (fwd_stages<D>() == 3 ? 3 : 2) : 1; }
+// Resident workgroups per CU: D = 128 one (128 KB of LDS); D = 64 three (or
+// two with four stages); D = 32 four (32 KB, at most 128 registers per wave).
+template <int D> constexpr int fwd_occupancy() {
+  return D == 64 ? (fwd_stages<D>() == 3 ? 3 : 2) : (D == 32 ? 4 : 1);
+}
 
 template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(const KParams p) {
@@ -76,12 +80,9 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
   // Operand read-ahead, in steps.  D = 128: a whole region (16) without
   // score_mod, 8 with it (16 would spill there); measured 2-3 % (8 vs 4) and
   // another 1-2.5 % (16 vs 8) at the headline shapes.  D = 64: 4 (three waves
-  // per SIMD, 168 registers each).
-#ifdef SIGATTN_FWD_LA128
-  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : SIGATTN_FWD_LA128) : 4;
-#else
-  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : 16) : 4;
-#endif
+  // per SIMD, 168 registers each); D = 32: 4, a whole region (2 with
+  // score_mod, which spills at four waves per SIMD otherwise).
+  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : 16) : (D == 32 && SCOREMOD ? 2 : 4);
   constexpr int NWD = 8 * NCB;          // packed P words per block
   constexpr int BAR = NSTEP - LA;       // step of the tile barrier in odd regions
   static_assert(NSTEP % LA == 0, "region shape");
@@ -421,11 +422,6 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
       }
     }
 
-#ifdef SIGATTN_FWD_AGPR
-    // Any AGPR operand makes the compiler select the MFMA form whose
-    // accumulators (srcC / vdst) live in AGPRs.
-    asm volatile("" ::"a"(acc[0][0][0]));
-#endif
     if (!CAUSAL && p.rsplit > 1 &&
         !split_combine<NCB * NDB, NWV>([&](int i) SIGATTN_INLINE -> f32x16 & { return acc[i / NDB][i % NDB]; },
                                        p.rs_part + (int64_t)ritem * p.rsplit * (BM * D), p.rs_cnt + ritem,
@@ -492,11 +488,13 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
 // and 5-13 % padded.
 template <typename T, int D>
 static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
-  launch_fwd_w<T, D, (D == 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
+  launch_fwd_w<T, D, (D <= 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
 }
 
-int fwd_rows_per_workgroup(int D) { return (D == 64 ? 4 : 8) * 32; }
-int fwd_workgroups_per_cu(int D) { return D == 64 ? fwd_occupancy<64>() : fwd_occupancy<128>(); }
+int fwd_rows_per_workgroup(int D) { return (D <= 64 ? 4 : 8) * 32; }
+int fwd_workgroups_per_cu(int D) {
+  return D == 32 ? fwd_occupancy<32>() : (D == 64 ? fwd_occupancy<64>() : fwd_occupancy<128>());
+}
 
 __global__ __launch_bounds__(256) void rs_clear_kernel(int *a, int na, int *b, int nb) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < na + nb; i += gridDim.x * 256) {
@@ -513,10 +511,12 @@ void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool score
                      hipStream_t st) {
   if (dtype == kBF16) {
     if (D == 128) launch_fwd_t<__bf16, 128>(p, causal, scoremod, st);
-    else launch_fwd_t<__bf16, 64>(p, causal, scoremod, st);
+    else if (D == 64) launch_fwd_t<__bf16, 64>(p, causal, scoremod, st);
+    else launch_fwd_t<__bf16, 32>(p, causal, scoremod, st);
   } else {
     if (D == 128) launch_fwd_t<_Float16, 128>(p, causal, scoremod, st);
-    else launch_fwd_t<_Float16, 64>(p, causal, scoremod, st);
+    else if (D == 64) launch_fwd_t<_Float16, 64>(p, causal, scoremod, st);
+    else launch_fwd_t<_Float16, 32>(p, causal, scoremod, st);
   }
 }
 
