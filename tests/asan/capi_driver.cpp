@@ -15,6 +15,7 @@
 namespace {
 std::vector<std::string> g_calls;
 sigattn::KParams g_last{};
+int g_D = 0;  // head dim passed to the last kernel launch
 int g_fail = 0;
 
 void record(const char *name, const sigattn::KParams &p) {
@@ -56,16 +57,32 @@ std::string calls() {
 }  // namespace
 
 namespace sigattn {
-void launch_fwd_mfma(const KParams &p, int, int, bool, bool, hipStream_t) { record("fwd_mfma", p); }
-void launch_bwd_dq_mfma(const KParams &p, int, int, bool, bool, hipStream_t) { record("dq_mfma", p); }
-void launch_bwd_dkdv_mfma(const KParams &p, int, int, bool, bool, bool dsout, hipStream_t) {
+void launch_fwd_mfma(const KParams &p, int, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("fwd_mfma", p);
+}
+void launch_bwd_dq_mfma(const KParams &p, int, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("dq_mfma", p);
+}
+void launch_bwd_dkdv_mfma(const KParams &p, int, int D, bool, bool, bool dsout, hipStream_t) {
+  g_D = D;
   record(dsout ? "dkdv_mfma_ds" : "dkdv_mfma", p);
 }
 void launch_bwd_dq_ds_mfma(const KParams &p, int, int, bool, hipStream_t) { record("dq_ds", p); }
 void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record("fwd_splitkv", p); }
-void launch_fwd_generic(const KParams &p, int, int, bool, hipStream_t) { record("fwd_generic", p); }
-void launch_bwd_dq_generic(const KParams &p, int, int, bool, hipStream_t) { record("dq_generic", p); }
-void launch_bwd_dkdv_generic(const KParams &p, int, int, bool, hipStream_t) { record("dkdv_generic", p); }
+void launch_fwd_generic(const KParams &p, int, int D, bool, hipStream_t) {
+  g_D = D;
+  record("fwd_generic", p);
+}
+void launch_bwd_dq_generic(const KParams &p, int, int D, bool, hipStream_t) {
+  g_D = D;
+  record("dq_generic", p);
+}
+void launch_bwd_dkdv_generic(const KParams &p, int, int D, bool, hipStream_t) {
+  g_D = D;
+  record("dkdv_generic", p);
+}
 int fwd_rows_per_workgroup(int D) { return (D == 64 ? 4 : 8) * 32; }
 int fwd_workgroups_per_cu(int D) { return D == 64 ? 3 : 1; }
 int bwd_dq_rows_per_workgroup() { return 128; }
@@ -186,12 +203,24 @@ int main() {
   {
     // D = 32 in bf16: the MFMA kernels, recompute backward (no two-pass workspace).
     sigattn_problem p = base(1, 40, 1, 32);
-    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma");
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_D == 32 && g_last.dmem == 32);
     EXPECT(sigattn_bwd_workspace_bytes(&p) == 0);
     EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
-    // fp32, D = 16, misaligned strides: the portable kernels.
-    p.D = 16;
-    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");
+    // D = 16 in bf16: the D = 32 kernels on 16-column rows.
+    p = base(1, 40, 2, 16);
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_mfma" && g_D == 32 && g_last.dmem == 16);
+    EXPECT(sigattn_bwd_workspace_bytes(&p) == 0 && sigattn_fwd_workspace_bytes(&p) == 0);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma" &&
+           g_D == 32 && g_last.dmem == 16);
+    // fp32 or misaligned rows at D = 16: the portable kernels.
+    p.dtype = SIGATTN_F32;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic" && g_D == 16);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_generic,dkdv_generic" &&
+           g_D == 16);
+    p.dtype = SIGATTN_BF16;
+    p.q_stride_t = 36;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic" && g_D == 16);
+    p = base(1, 40, 1, 32);
     p.D = 64;
     p.dtype = SIGATTN_F32;
     EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_generic,dkdv_generic");

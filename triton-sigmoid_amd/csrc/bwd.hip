@@ -71,8 +71,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     key0 = split_tile(rchunk, p.rsplit, ntk) * BN;
     Lk = min(Lk, split_tile(rchunk + 1, p.rsplit, ntk) * BN) - key0;
   }
+  const bool half = p.half_head(D);  // head_dim 16 in this D = 32 kernel
   // Padding item: its zero rows as part of one contiguous span (see zero_row_span).
-  if (qb * BM >= Lq && p.q_rows_contiguous(D)) {
+  if (qb * BM >= Lq && p.q_rows_contiguous(half ? 16 : D)) {
     zero_row_span((uint16_t *)p.dq + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
                   threadIdx.x, 256);
     return;
@@ -106,8 +107,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     const uint16_t *orow = dOb + (int64_t)my_q * p.sq_t + 8 * hi;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      qf[s] = ok ? *(const u32x4 *)(qr + 16 * s) : zero4();
-      of[s] = ok ? *(const u32x4 *)(orow + 16 * s) : zero4();
+      const bool in = ok && !(half && s > 0);
+      qf[s] = in ? *(const u32x4 *)(qr + 16 * s) : zero4();
+      of[s] = in ? *(const u32x4 *)(orow + 16 * s) : zero4();
     }
   }
   f32x16 acc[NDB];
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   TileOffsets<D> to;
   to.init(lane);
   DmaPlan<BN, D, 4> dma;
-  dma.init(w, lane);
+  dma.init(w, lane, half);
   const int kv_stride_bytes = (int)(p.sk_t * 2);
 
   // dS of one 32-key block into eight packed words.
@@ -230,6 +232,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (half && g >= 2) break;  // columns 16..31: not in the tensor
         const int d0 = db * 32 + 8 * g + 4 * hi;
         u32x2 o;
         o.x = Elem<T>::pack(acc[db][4 * g] * scale, acc[db][4 * g + 1] * scale);
@@ -297,8 +300,9 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   }
   const int Lq = p.len_q(b);
   const int Lk = p.len_k(b);
+  const bool half = p.half_head(D);  // head_dim 16 in this D = 32 kernel
   // Padding item: its zero dK and dV rows as part of contiguous spans (see zero_row_span).
-  if (kblk * BN >= Lk && p.k_rows_contiguous(D)) {
+  if (kblk * BN >= Lk && p.k_rows_contiguous(half ? 16 : D)) {
     const int r1 = min(kblk * BN + BN, p.Tk);
     zero_row_span((uint16_t *)p.dk + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 256);
     zero_row_span((uint16_t *)p.dv + (int64_t)b * p.sk_b, p.sk_t, kblk * BN, r1, h, p.H, threadIdx.x, 256);
@@ -344,8 +348,9 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     const uint16_t *vr = Vb + (int64_t)my_k * p.sk_t + 8 * hi;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      kf[s] = kok ? *(const u32x4 *)(kr + 16 * s) : zero4();
-      vf[s] = kok ? *(const u32x4 *)(vr + 16 * s) : zero4();
+      const bool in = kok && !(half && s > 0);
+      kf[s] = in ? *(const u32x4 *)(kr + 16 * s) : zero4();
+      vf[s] = in ? *(const u32x4 *)(vr + 16 * s) : zero4();
     }
   }
   // Consume the K / V loads before the loop, so the compiler's wait for them
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   TileOffsets<D> to;
   to.init(lane);
   DmaPlan<BMQ, D, 4> dma;
-  dma.init(w, lane);
+  dma.init(w, lane, half);
   const int q_stride_bytes = (int)(p.sq_t * 2);
   auto issue = [&](int st, int t) SIGATTN_INLINE {
     dma.issue(sQ[st], Qb + (int64_t)mstart * p.sq_t, q_stride_bytes, t * BMQ, mend - mstart);
@@ -589,6 +594,7 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (half && g >= 2) break;  // columns 16..31: not in the tensor
         const int d0 = db * 32 + 8 * g + 4 * hi;
         u32x2 ok_, ov;
         ok_.x = Elem<T>::pack(dka[db][4 * g] * scale, dka[db][4 * g + 1] * scale);

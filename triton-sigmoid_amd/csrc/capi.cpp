@@ -49,6 +49,7 @@ KParams make_params(const sigattn_problem *p) {
   k.H = (int)p->H;
   k.Tq = (int)p->Tq;
   k.Tk = (int)p->Tk;
+  k.dmem = (int)p->D;
   return k;
 }
 
@@ -57,13 +58,13 @@ bool rows_fit_2g(int64_t T, int64_t stride) {
   return stride == 0 || T <= (((int64_t)1 << 30) - 1) / stride;
 }
 
-// True when the MFMA kernels can take the problem: 16-bit elements, D of 32,
-// 64 or 128, every row start 16-byte aligned, and every row of a sequence
+// True when the MFMA kernels can take the problem: 16-bit elements, D of 16,
+// 32, 64 or 128, every row start 16-byte aligned, and every row of a sequence
 // within 2^31 bytes of the sequence's first row (the tile copies address rows
 // with a 32-bit byte offset from that row).
 bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
   if (p->dtype == SIGATTN_F32) return false;
-  if (p->D != 32 && p->D != 64 && p->D != 128) return false;
+  if (!is_pow2_head_dim(p->D)) return false;
   if (!rows_fit_2g(p->Tq, p->q_stride_t) || !rows_fit_2g(p->Tk, p->k_stride_t)) return false;
   const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
                               p->k_stride_b, p->k_stride_t, p->k_stride_h};
@@ -89,8 +90,12 @@ struct SplitPlan {
 #endif
 
 // The split-KV kernel and the two-pass backward exist at D = 64 and 128; at
-// D = 32 the main forward and the recompute backward serve every shape.
+// D = 16 and 32 the main forward and the recompute backward serve every shape.
 bool wide_head(const sigattn_problem *p) { return p->D == 64 || p->D == 128; }
+
+// Head dim of the MFMA kernel instance: head_dim 16 runs in the D = 32
+// kernels (KParams::dmem = 16).
+int mfma_head_dim(const sigattn_problem *p) { return p->D == 16 ? 32 : (int)p->D; }
 
 SplitPlan splitkv_plan(const sigattn_problem *p, bool mfma) {
   SplitPlan sp;
@@ -409,7 +414,7 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     k.chunk = sp.chunk;
     sigattn::launch_fwd_splitkv(k, p->dtype, (int)p->D, p->score_mod != nullptr, st);
   } else if (mfma) {
-    sigattn::launch_fwd_mfma(k, p->dtype, (int)p->D, p->causal != 0, p->score_mod != nullptr, st);
+    sigattn::launch_fwd_mfma(k, p->dtype, mfma_head_dim(p), p->causal != 0, p->score_mod != nullptr, st);
   } else {
     sigattn::launch_fwd_generic(k, p->dtype, (int)p->D, p->causal != 0, st);
   }
@@ -481,7 +486,7 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   k.dv = dv;
   const hipStream_t st = (hipStream_t)stream;
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
-  const int dt = p->dtype, D = (int)p->D;
+  const int dt = p->dtype, D = mfma ? mfma_head_dim(p) : (int)p->D;
   (void)hipGetLastError();
   zero_packed_gaps(p, parts != kBwdDkdv ? dq : nullptr, parts != kBwdDq ? dk : nullptr,
                    parts != kBwdDq ? dv : nullptr, st);

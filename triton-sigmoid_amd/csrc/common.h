@@ -102,6 +102,14 @@ struct KParams {
   float *rs_part;
   int *rs_cnt;
   int ncu;  // compute units of the device (WorkOrder::by_level's dealing rounds)
+  // Head dim of the tensors.  The D = 32 kernels also take head_dim 16
+  // (dmem = 16): the stationary rows' upper 16 columns enter as zeros, the
+  // streamed tiles repeat the 16 columns there (so every product over the
+  // head dim adds exact zeros), and only the first 16 output columns are
+  // stored.
+  int dmem;
+  // The D = 32 kernels computing head_dim 16 (see dmem).
+  __device__ __forceinline__ bool half_head(int D) const { return D == 32 && dmem == 16; }
 
   // Valid query / key rows of batch b.
   __device__ __forceinline__ int len_q(int b) const {
@@ -538,12 +546,15 @@ template <int ROWS, int D, int NWAVES> struct DmaPlan {
   int cbyte[NI];     // byte offset of the swizzled source chunk within its row
   int r0[NI];        // first tile row of each instruction (wave-uniform)
 
-  __device__ __forceinline__ void init(int wave, int lane) {
+  // half: the row holds D / 2 elements (head_dim 16 in a D = 32 tile); the
+  // tile's upper chunks repeat its lower ones.
+  __device__ __forceinline__ void init(int wave, int lane, bool half = false) {
+    const int cmask = half ? CPR / 2 - 1 : CPR - 1;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       r0[i] = (wave * NI + i) * RPI;
       row[i] = r0[i] + lane / CPR;
-      cbyte[i] = 16 * ((lane % CPR) ^ swz<D>(row[i]));
+      cbyte[i] = 16 * (((lane % CPR) ^ swz<D>(row[i])) & cmask);
     }
   }
   // base: uniform pointer to row 0 of the (batch, head) slice.

@@ -149,7 +149,8 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
     }
     // Padding item (the row block lies wholly past seq_lens_q): its zero rows
     // as part of one contiguous span over all heads when the layout allows.
-    if (qb * BM >= Lq && nitems == 1 && p.q_rows_contiguous(D)) {
+    const bool half = p.half_head(D);  // head_dim 16 in this D = 32 kernel
+    if (qb * BM >= Lq && nitems == 1 && p.q_rows_contiguous(half ? 16 : D)) {
       zero_row_span((uint16_t *)p.out + (int64_t)b * p.sq_b, p.sq_t, qb * BM, min(qb * BM + BM, p.Tq), h, p.H,
                     threadIdx.x, 64 * NWV);
       return;
@@ -191,7 +192,8 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
       const bool ok = q < Lq;
       const uint16_t *qrow = Qb + (int64_t)q * p.sq_t + 8 * hi;
   #pragma unroll
-      for (int s = 0; s < NKS; ++s) qf[c][s] = ok ? *(const u32x4 *)(qrow + 16 * s) : zero4();
+      for (int s = 0; s < NKS; ++s)
+        qf[c][s] = ok && !(half && s > 0) ? *(const u32x4 *)(qrow + 16 * s) : zero4();
     }
     // Consume the Q loads here, so the compiler's wait for them is not placed
     // at the head of the key loop, where it would also wait for the tile copies.
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
     TileOffsets<D> to;
     to.init(lane);
     DmaPlan<BN, D, NWV> dma;
-    dma.init(w, lane);
+    dma.init(w, lane, half);
     const int kv_stride_bytes = (int)(p.sk_t * 2);
 
     float creg = 0.0f;
@@ -439,6 +441,7 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
         for (int db = 0; db < NDB; ++db) {
   #pragma unroll
           for (int g = 0; g < 4; ++g) {
+            if (half && g >= 2) break;  // columns 16..31: not in the tensor
             const int d0 = db * 32 + 8 * g + 4 * hi;
             u32x2 o;
             o.x = Elem<T>::pack(acc[c][db][4 * g + 0], acc[c][db][4 * g + 1]);
