@@ -71,6 +71,18 @@ void launch_bwd_dkdv_mfma(const KParams &p, int, int D, bool, bool, bool dsout, 
 }
 void launch_bwd_dq_ds_mfma(const KParams &p, int, int, bool, hipStream_t) { record("dq_ds", p); }
 void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record("fwd_splitkv", p); }
+void launch_fwd_f32(const KParams &p, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("fwd_f32", p);
+}
+void launch_bwd_dq_f32(const KParams &p, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("dq_f32", p);
+}
+void launch_bwd_dkdv_f32(const KParams &p, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("dkdv_f32", p);
+}
 void launch_fwd_generic(const KParams &p, int, int D, bool, hipStream_t) {
   g_D = D;
   record("fwd_generic", p);
@@ -119,7 +131,61 @@ extern "C" hipError_t hipDeviceGetAttribute(int *value, hipDeviceAttribute_t, in
   return hipSuccess;
 }
 
+// The fp32 kernels' LDS tiles (32 rows x D floats, four waves copying): the
+// tile copies place each global element exactly once, at the offset
+// F32Tile<D>::elem reads it from; F32RowReads<D> agrees with elem for every
+// lane and (g, r, db); the head-dim products' 16-byte reads of 16
+// consecutive rows at one piece position fall in 16 different bank groups
+// (64 banks of 4 bytes); with half rows (head_dim 16 in the D = 32 tiles)
+// the upper 16 columns repeat the lower 16.
+template <int D> void check_f32_tiles() {
+  using sigattn::DmaPlan;
+  using sigattn::F32RowReads;
+  using sigattn::F32Tile;
+  constexpr int ROWS = 32, CPR = D / 4;
+  for (int half = 0; half < (D == 32 ? 2 : 1); ++half) {
+    std::vector<int> src(ROWS * D, -1);  // LDS float -> global (row, column) it holds
+    for (int w = 0; w < 4; ++w)
+      for (int lane = 0; lane < 64; ++lane) {
+        DmaPlan<ROWS, 2 * D, 4> dp;
+        dp.init(w, lane, half != 0);
+        for (int i = 0; i < DmaPlan<ROWS, 2 * D, 4>::NI; ++i) {
+          const int row = dp.r0[i] + lane / CPR, slot = lane % CPR;
+          EXPECT(row == dp.row[i] && dp.cbyte[i] % 16 == 0);
+          for (int e = 0; e < 4; ++e) {
+            const int at = row * D + 4 * slot + e;
+            EXPECT(src[at] == -1);
+            src[at] = row * D + 4 * (dp.cbyte[i] / 16) + e;
+          }
+        }
+      }
+    for (int r = 0; r < ROWS; ++r)
+      for (int d = 0; d < D; ++d) {
+        const int want = r * D + (half ? d % 16 : d);
+        EXPECT(src[F32Tile<D>::elem(r, d)] == want);
+      }
+  }
+  for (int lane = 0; lane < 64; ++lane) {
+    F32RowReads<D> rr;
+    rr.init(lane & 31, lane >> 5);
+    for (int g = 0; g < 4; ++g)
+      for (int r = 0; r < 4; ++r)
+        for (int db = 0; db < D / 32; ++db)
+          EXPECT(rr.at(g, r, db) == F32Tile<D>::elem(8 * g + 4 * (lane >> 5) + r, 32 * db + (lane & 31)));
+  }
+  for (int r0 = 0; r0 < ROWS; r0 += 16)
+    for (int c = 0; c < CPR; ++c) {
+      unsigned groups = 0;
+      for (int r = r0; r < r0 + 16; ++r) groups |= 1u << ((F32Tile<D>::piece(r, c) / 4) % 16);
+      EXPECT(groups == 0xffffu);
+    }
+}
+
 int main() {
+  check_f32_tiles<32>();
+  check_f32_tiles<64>();
+  check_f32_tiles<128>();
+
   // --- validation: the error codes of tests/test_capi_cpu.py, for every entry point
   struct Bad {
     const char *what;
@@ -212,8 +278,15 @@ int main() {
     EXPECT(sigattn_bwd_workspace_bytes(&p) == 0 && sigattn_fwd_workspace_bytes(&p) == 0);
     EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma" &&
            g_D == 32 && g_last.dmem == 16);
-    // fp32 or misaligned rows at D = 16: the portable kernels.
+    // fp32 at D = 16: the fp32 MFMA kernels' D = 32 instances, likewise.
     p.dtype = SIGATTN_F32;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_f32" && g_D == 32 && g_last.dmem == 16);
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_f32,dkdv_f32" &&
+           g_D == 32 && g_last.dmem == 16);
+    EXPECT(sigattn_bwd_workspace_bytes(&p) == 0 && sigattn_fwd_workspace_bytes(&p) == 0);
+    // Rows not 16-byte aligned: the portable kernels (a row stride of 4k + 2
+    // floats, or of 8k + 4 16-bit elements).
+    p.q_stride_t = 34;
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic" && g_D == 16);
     EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_generic,dkdv_generic" &&
            g_D == 16);
@@ -223,8 +296,17 @@ int main() {
     p = base(1, 40, 1, 32);
     p.D = 64;
     p.dtype = SIGATTN_F32;
-    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_generic,dkdv_generic");
+    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_f32,dkdv_f32" && g_D == 64);
     EXPECT(sigattn_bwd_workspace_bytes(&p) == 0);
+    // A misaligned pointer sends fp32 to the portable kernels too.
+    EXPECT(sigattn_fwd(&p, (char *)kFake + 4, nullptr) == 0 && calls() == "fwd_generic");
+    // fp32 rows spanning 2^31 bytes or more (the copies' 32-bit offsets): portable.
+    p.Tq = p.Tk = (1 << 28) / 64 + 1;
+    p.q_stride_t = p.k_stride_t = 128;
+    p.q_stride_b = p.k_stride_b = p.Tq * 128;
+    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");
+    p = base(1, 40, 1, 32);
+    p.D = 64;
     p.dtype = SIGATTN_F16;
     p.q_stride_t = 68;
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "fwd_generic");

@@ -58,7 +58,7 @@ DENSE = [  # (B, T, H, D, dtype, causal)
     (2, 384, 4, 128, torch.bfloat16, False),  # two-pass backward
     (1, 2048, 2, 128, torch.bfloat16, False), # range split forward and dQ
     (1, 300, 3, 128, torch.bfloat16, True),
-    (2, 77, 2, 32, torch.float32, False),     # portable kernels
+    (2, 77, 2, 32, torch.float32, False),     # fp32 MFMA kernels
     (1, 16, 2, 64, torch.bfloat16, False),    # decode-sized queries
 ]
 

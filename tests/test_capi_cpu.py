@@ -256,7 +256,7 @@ def test_empty_problems_return_before_any_launch():
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
-@pytest.mark.parametrize("src", ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip"])
+@pytest.mark.parametrize("src", ["fwd.hip", "bwd.hip", "decode.hip", "f32.hip", "generic.hip"])
 def test_device_code_has_no_packed_fp32_instructions(src):
     """Every HIP source is built with packed-fp32 selection disabled; check the
     gfx950 assembly of each kernel file."""
@@ -265,6 +265,8 @@ def test_device_code_has_no_packed_fp32_instructions(src):
            str(_build.CSRC / src), "-o", "-"]
     asm = subprocess.run(cmd, capture_output=True, text=True, check=True).stdout
     assert "v_mfma" in asm or src == "generic.hip"
+    if src == "f32.hip":
+        assert "v_mfma_f32_32x32x2_f32" in asm
     assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)
     # The range split's arrival counter (split_combine) is an agent-scope
     # acquire-release atomic: in every kernel that counts, the add sits

@@ -45,11 +45,12 @@ def _clean(t, lens):
 
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("D", [16, 32, 64, 128])
 @pytest.mark.parametrize("Tq,Tk", [(1, 256), (1, 4099), (5, 1000), (32, 20000), (17, 300)])
 def test_decode_matches_oracle(dtype, D, Tq, Tk):
-    # D = 16 and 32 have no split-KV kernel: one MFMA forward workgroup per 128 queries.
+    # D = 16 and 32, and fp32, have no split-KV kernel: one MFMA forward
+    # workgroup per 128 queries.
     B, H = 3, 4
     q, k, v, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=Tq * 1000 + Tk + D)
     o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk.to(DEV), seq_lens_q=sq.to(DEV))

@@ -67,7 +67,7 @@ def test_various_num_heads_match_oracle(H, D):
     assert_close_to_oracle(v.grad, dv, dtype, "dV")
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("D", [16, 32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_dense_score_mod_matches_oracle(dtype, D, causal):
@@ -202,7 +202,7 @@ def test_reference_grid_long_shapes(B, T, H):
 def test_c1_fp32_matches_oracle(causal):
     """fp32 B=2 L=256 H=4 D=64, q/k/v/dO ~ N(0,1)
     from a seed, scale 1/sqrt(D), default bias -log(L), fwd+bwd through the
-    public API (the portable fp32 kernels) against the float64 oracle."""
+    public API (the fp32 MFMA kernels) against the float64 oracle."""
     B, T, H, D = 2, 256, 4, 64
     q, k, v, do = _inputs(B, T, H, D, torch.float32, seed=0)
     for t in (q, k, v):
@@ -216,6 +216,36 @@ def test_c1_fp32_matches_oracle(causal):
     assert_close_to_oracle(q.grad, dq, torch.float32, "dQ")
     assert_close_to_oracle(k.grad, dk, torch.float32, "dK")
     assert_close_to_oracle(v.grad, dv, torch.float32, "dV")
+
+
+def _off_boundary(t):
+    """A contiguous copy of t whose data starts one element past a 16-byte
+    boundary (a view one element into its storage), as a leaf."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    buf[1:].copy_(t.reshape(-1))
+    return buf[1:].view(t.shape).detach()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_rows_off_16_byte_boundaries_match_oracle(dtype, causal):
+    """Q, K, V and dO whose rows do not start on 16-byte boundaries cannot be
+    copied into LDS by the MFMA kernels' 16-byte tile copies; the portable
+    kernels take them, with the same results."""
+    B, T, H, D = 2, 130, 3, 64
+    q, k, v, do = (_off_boundary(t) for t in _inputs(B, T, H, D, dtype, seed=21))
+    assert all(t.data_ptr() % 16 != 0 for t in (q, k, v, do))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=causal)
+    o.backward(do)
+    bias = np.full(B, -math.log(T), dtype=np.float32).astype(np.float64)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1.0 / math.sqrt(D)), bias=bias,
+                                          causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
 
 
 # --- behaviour -----------------------------------------------------------------

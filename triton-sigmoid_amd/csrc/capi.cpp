@@ -58,21 +58,34 @@ bool rows_fit_2g(int64_t T, int64_t stride) {
   return stride == 0 || T <= (((int64_t)1 << 30) - 1) / stride;
 }
 
-// True when the MFMA kernels can take the problem: 16-bit elements, D of 16,
-// 32, 64 or 128, every row start 16-byte aligned, and every row of a sequence
-// within 2^31 bytes of the sequence's first row (the tile copies address rows
-// with a 32-bit byte offset from that row).
-bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
-  if (p->dtype == SIGATTN_F32) return false;
-  if (!is_pow2_head_dim(p->D)) return false;
-  if (!rows_fit_2g(p->Tq, p->q_stride_t) || !rows_fit_2g(p->Tk, p->k_stride_t)) return false;
+// Every row start 16-byte aligned (strides in elements of `esize` bytes) and
+// every row of a sequence within 2^31 bytes of the sequence's first row (the
+// tile copies address rows with a 32-bit byte offset from that row).
+bool rows_dma_ready(const sigattn_problem *p, const void *const *ptrs, int nptr, int esize) {
+  const int64_t per16 = 16 / esize, half_units = esize / 2;
+  if (!rows_fit_2g(p->Tq, half_units * p->q_stride_t) || !rows_fit_2g(p->Tk, half_units * p->k_stride_t))
+    return false;
   const int64_t strides[6] = {p->q_stride_b, p->q_stride_t, p->q_stride_h,
                               p->k_stride_b, p->k_stride_t, p->k_stride_h};
   for (int64_t s : strides)
-    if (s % 8 != 0) return false;
+    if (s % per16 != 0) return false;
   for (int i = 0; i < nptr; ++i)
     if (ptrs[i] && !aligned16(ptrs[i])) return false;
   return true;
+}
+
+// True when the 16-bit MFMA kernels can take the problem: f16 / bf16, D of
+// 16, 32, 64 or 128, rows as rows_dma_ready requires.
+bool use_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
+  if (p->dtype == SIGATTN_F32 || !is_pow2_head_dim(p->D)) return false;
+  return rows_dma_ready(p, ptrs, nptr, 2);
+}
+
+// True when the fp32 MFMA kernels (v_mfma_f32_32x32x2_f32) can take the
+// problem: fp32, D of 16, 32, 64 or 128, rows as rows_dma_ready requires.
+bool use_f32_mfma(const sigattn_problem *p, const void *const *ptrs, int nptr) {
+  if (p->dtype != SIGATTN_F32 || !is_pow2_head_dim(p->D)) return false;
+  return rows_dma_ready(p, ptrs, nptr, 4);
 }
 
 // Split-KV forward plan: nsplit = 0 when the main forward kernel takes the
@@ -415,6 +428,8 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     sigattn::launch_fwd_splitkv(k, p->dtype, (int)p->D, p->score_mod != nullptr, st);
   } else if (mfma) {
     sigattn::launch_fwd_mfma(k, p->dtype, mfma_head_dim(p), p->causal != 0, p->score_mod != nullptr, st);
+  } else if (use_f32_mfma(p, ptrs, 4)) {
+    sigattn::launch_fwd_f32(k, mfma_head_dim(p), p->causal != 0, p->score_mod != nullptr, st);
   } else {
     sigattn::launch_fwd_generic(k, p->dtype, (int)p->D, p->causal != 0, st);
   }
@@ -458,6 +473,7 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   const bool need_dkdv = parts != kBwdDq && p->Tk > 0;
   const void *ptrs[7] = {p->q, p->k, p->v, dout, dq, dk, dv};
   const bool mfma = use_mfma(p, ptrs, 7);
+  const bool f32mma = use_f32_mfma(p, ptrs, 7);
 
   // Two-pass backward when a workspace holds the dS of at least one head.
   // The halves (kBwdDq, kBwdDkdv) need the whole problem's dS at once: the
@@ -486,7 +502,7 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   k.dv = dv;
   const hipStream_t st = (hipStream_t)stream;
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
-  const int dt = p->dtype, D = mfma ? mfma_head_dim(p) : (int)p->D;
+  const int dt = p->dtype, D = mfma || f32mma ? mfma_head_dim(p) : (int)p->D;
   (void)hipGetLastError();
   zero_packed_gaps(p, parts != kBwdDkdv ? dq : nullptr, parts != kBwdDq ? dk : nullptr,
                    parts != kBwdDq ? dv : nullptr, st);
@@ -511,10 +527,12 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   // concurrently on two streams only made both slower (measured).
   if (need_dq) {
     if (mfma) sigattn::launch_bwd_dq_mfma(k, dt, D, causal, sm, st);
+    else if (f32mma) sigattn::launch_bwd_dq_f32(k, D, causal, sm, st);
     else sigattn::launch_bwd_dq_generic(k, dt, D, causal, st);
   }
   if (need_dkdv) {
     if (mfma) sigattn::launch_bwd_dkdv_mfma(k, dt, D, causal, sm, false, st);
+    else if (f32mma) sigattn::launch_bwd_dkdv_f32(k, D, causal, sm, st);
     else sigattn::launch_bwd_dkdv_generic(k, dt, D, causal, st);
   }
   return launch_status();

@@ -482,8 +482,8 @@ __device__ __forceinline__ float acc_read(float v) {
 // swz(r) = 4*((r>>1)&1) + ((r>>2)&3), and D = 32 (4 chunks per row, four
 // rows per line) swz(r) = (r>>2)&3: in each case any 16 consecutive rows read
 // at one logical chunk land on 16 distinct 16-byte slots of a line.
-template <int D> __device__ __forceinline__ int swz(int row) {
-  if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
+template <int D> __host__ __device__ __forceinline__ int swz(int row) {
+  if constexpr (D >= 128) return 4 * (row & 3) + ((row >> 2) & 3);
   else if constexpr (D == 64) return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
   else return (row >> 2) & 3;
 }
@@ -548,7 +548,7 @@ template <int ROWS, int D, int NWAVES> struct DmaPlan {
 
   // half: the row holds D / 2 elements (head_dim 16 in a D = 32 tile); the
   // tile's upper chunks repeat its lower ones.
-  __device__ __forceinline__ void init(int wave, int lane, bool half = false) {
+  __host__ __device__ __forceinline__ void init(int wave, int lane, bool half = false) {
     const int cmask = half ? CPR / 2 - 1 : CPR - 1;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -579,6 +579,38 @@ template <int ROWS, int D, int NWAVES> struct DmaPlan {
                    : "v"(off), "s"(base), "{m0}"(dst)
                    : "memory");
     }
+  }
+};
+
+// fp32 tiles of rows x D floats in LDS, filled by DmaPlan<rows, 2D, waves>
+// (the same bytes as a 16-bit tile of 2D elements): 16-byte piece c of row
+// r sits at piece c ^ swz<2D>(r), so each group of 16 rows read at one piece
+// position covers every bank once.  Offsets are in floats.
+template <int D> struct F32Tile {
+  static __host__ __device__ __forceinline__ int piece(int r, int c) { return r * D + 4 * (c ^ swz<2 * D>(r)); }
+  static __host__ __device__ __forceinline__ int elem(int r, int d) { return piece(r, d >> 2) + (d & 3); }
+};
+
+// Per-lane offsets of the fp32 kernels' row-product reads: element
+// (8g + 4hi + r, 32db + l32) of an F32Tile, for lane l32 + 32hi and every
+// (g, r, db), is o[g & 1][j] plus a compile-time constant (j = r & 1 when
+// D >= 64, r >> 1 when D = 32).  The swizzle term there splits as
+// swz<2D>(8g + 4hi + r) = 8(r >> 1) + 4(r & 1) + m (D >= 64) or 4(r >> 1) + m
+// (D = 32) with m = (2g + hi) & 3 depending on g only through g & 1, and its
+// bits above 2 only move whole 32-float column blocks (db ^ (r >> 1)).
+template <int D> struct F32RowReads {
+  int o[2][2];
+  __host__ __device__ __forceinline__ void init(int l32, int hi) {
+    const int x = l32 >> 2;
+#pragma unroll
+    for (int gp = 0; gp < 2; ++gp)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        o[gp][j] = 4 * hi * D + 4 * (x ^ ((2 * gp + hi) & 3) ^ (4 * j)) + (l32 & 3);
+  }
+  __host__ __device__ __forceinline__ int at(int g, int r, int db) const {
+    const int j = D >= 64 ? (r & 1) : (r >> 1);
+    return o[g & 1][j] + (8 * g + r) * D + (D >= 64 ? 32 * (db ^ (r >> 1)) : 0);
   }
 };
 

@@ -69,6 +69,12 @@ struct GapAxis {
 // one launch (an axis with rows = 0 takes no workgroups); esize = 2 or 4.
 void launch_zero_gaps(const GapAxis &a, const GapAxis &b, int esize, hipStream_t st);
 
+// fp32 kernels on the matrix cores (v_mfma_f32_32x32x2_f32): D in {32, 64,
+// 128} (head_dim 16 as D = 32 with KParams::dmem = 16), 16-byte aligned rows.
+void launch_fwd_f32(const KParams &p, int D, bool causal, bool scoremod, hipStream_t st);
+void launch_bwd_dq_f32(const KParams &p, int D, bool causal, bool scoremod, hipStream_t st);
+void launch_bwd_dkdv_f32(const KParams &p, int D, bool causal, bool scoremod, hipStream_t st);
+
 // Portable kernels: any dtype, D in {16, 32, 64, 128}, any alignment.
 void launch_fwd_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
 void launch_bwd_dq_generic(const KParams &p, int dtype, int D, bool causal, hipStream_t st);

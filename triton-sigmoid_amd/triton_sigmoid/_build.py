@@ -26,7 +26,7 @@ INCLUDE = ROOT.parent / "include"
 LIB_PATH = PKG_DIR / "libsigattn.so"
 BUILD_DIR = ROOT / "_build"
 
-SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "capi.cpp"]
+SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "f32.hip", "generic.hip", "capi.cpp"]
 ARCH = "gfx950"
 AUTOGRAD_SOURCE = "torch_autograd.cpp"
 AUTOGRAD_NAME = "_sigattn_autograd"
