@@ -112,8 +112,8 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
 /*
  * Split-KV forward for decode shapes (no counterpart in the reference, whose
  * forward has one workgroup per 16..128 queries of a (batch, head) however
- * few queries there are).  A non-causal problem with Tq <= 32 and Tk >= 256
- * taking the MFMA kernels cuts each (batch, head)'s keys into chunks, one
+ * few queries there are).  A non-causal f16/bf16 problem at head_dim 64 or
+ * 128 with Tq <= 32 and Tk >= 256 taking the MFMA kernels cuts each (batch, head)'s keys into chunks, one
  * workgroup each, and sums the chunks' fp32 partials in a second kernel; the
  * partials need sigattn_fwd_workspace_bytes(p) bytes of device memory
  * (0 when the problem does not split).  sigattn_fwd_ws with workspace NULL (or
@@ -122,7 +122,8 @@ int sigattn_fwd(const sigattn_problem *p, void *out, void *stream);
  * chunks, fixed order) and matches sigattn_fwd within fp32 summation order.
  *
  * Range split of small dense grids (no counterpart in the reference): a
- * dense non-causal problem taking the MFMA kernels whose workgroups (one per
+ * dense non-causal f16/bf16 problem at head_dim 64 or 128 taking the MFMA
+ * kernels whose workgroups (one per
  * 128 or 256 queries of every (batch, head)) would leave at least half of
  * the GPU's compute units idle, runs each query block's keys as 2-4 chunks
  * of at least 512 keys in as many workgroups when the chunks save at least
@@ -172,7 +173,7 @@ int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
 /*
  * The recompute backward with the range split of small dense grids (no
  * counterpart in the reference): for a dense non-causal problem at head_dim
- * 64 or 128 taking the MFMA kernels, whose dQ or dK/dV grid would leave at
+ * 64 or 128 taking the f16/bf16 MFMA kernels, whose dQ or dK/dV grid would leave at
  * least half of the GPU's compute units idle, the dQ kernel runs each query
  * block's keys and (head_dim 64) the dK/dV kernel each key block's queries
  * as 2-4 chunks of at least 512 rows, saving at least 1024 rows of each
