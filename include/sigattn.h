@@ -165,7 +165,10 @@ int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream);
 /*
  * Recompute backward: dq (q strides), dk and dv (k strides) from dout
  * (q strides).  No atomics: results are bitwise deterministic.  Padded query
- * rows get dq = 0, padded key rows get dk = dv = 0.
+ * rows get dq = 0, padded key rows get dk = dv = 0.  Dense f16/bf16 problems
+ * at head_dim <= 64 whose dQ and dK/dV grids (128 rows per workgroup)
+ * together fit one workgroup per compute unit run both kernels' work as one
+ * launch, bit-identical to the two launches.
  */
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
                 void *dv, void *stream);

@@ -70,6 +70,10 @@ void launch_bwd_dkdv_mfma(const KParams &p, int, int D, bool, bool, bool dsout, 
   record(dsout ? "dkdv_mfma_ds" : "dkdv_mfma", p);
 }
 void launch_bwd_dq_ds_mfma(const KParams &p, int, int, bool, hipStream_t) { record("dq_ds", p); }
+void launch_bwd_fused_mfma(const KParams &p, int, int D, bool, bool, hipStream_t) {
+  g_D = D;
+  record("bwd_fused", p);
+}
 void launch_fwd_splitkv(const KParams &p, int, int, bool, hipStream_t) { record("fwd_splitkv", p); }
 void launch_fwd_f32(const KParams &p, int D, bool, bool, hipStream_t) {
   g_D = D;
@@ -406,7 +410,7 @@ int main() {
     EXPECT(sigattn_bwd_split(&p, kFake, nullptr, kFake, kFake, nullptr, 0, nullptr) == 0 &&
            calls() == "dkdv_mfma" && g_last.rsplit == 0);
     EXPECT(sigattn_bwd_split(&p, kFake, kFake, kFake, kFake, nullptr, 0, nullptr) == 0 &&
-           calls() == "dq_mfma,dkdv_mfma" && g_last.rsplit == 0);
+           calls() == "bwd_fused" && g_last.rsplit == 0);
     // Causal, padded, D = 128 backward, or grids that fill the GPU: no split.
     sigattn_problem c = p;
     c.causal = 1;
@@ -440,6 +444,32 @@ int main() {
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 512 + size_t(128) * 4 * 128 * 64 * 4);
     c = base(1, 2048, 8, 64);  // 128 items: two chunks
     EXPECT(sigattn_fwd_workspace_bytes(&c) == 512 + size_t(128) * 2 * 128 * 64 * 4);
+    // The recompute backward as one launch: dense, D <= 64 (16-bit), and the
+    // dQ and dK/dV grids together within one workgroup per CU.
+    for (int causal = 0; causal < 2; ++causal) {
+      c = base(2, 1024, 8, 64);  // c2: 128 + 128 workgroups
+      c.causal = causal;
+      EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "bwd_fused" && g_D == 64);
+      EXPECT(sigattn_bwd_split(&c, kFake, kFake, kFake, kFake, kFake, 1 << 20, nullptr) == 0 &&
+             calls() == "bwd_fused");
+      EXPECT(sigattn_bwd_ws(&c, kFake, kFake, kFake, kFake, nullptr, 0, nullptr) == 0 && calls() == "bwd_fused");
+      // Halves alone run their own kernel.
+      EXPECT(sigattn_bwd_dq(&c, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma");
+      EXPECT(sigattn_bwd_dkdv(&c, kFake, kFake, kFake, nullptr) == 0 && calls() == "dkdv_mfma");
+    }
+    c = base(2, 1024, 8, 16);
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "bwd_fused" && g_D == 32 &&
+           g_last.dmem == 16);
+    c = base(3, 1024, 8, 64);  // 384 workgroups: two launches
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    c = base(2, 1024, 8, 128);
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    c = base(2, 1024, 8, 64);
+    c.seq_lens_q = c.seq_lens_k = (const int32_t *)kFake;
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    c = base(2, 1024, 8, 64);
+    c.dtype = SIGATTN_F32;
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_f32,dkdv_f32");
     g_cus = 0;
   }
   if (g_fail == 0) std::printf("capi sanitizer driver: all checks passed\n");

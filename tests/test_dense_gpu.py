@@ -1,6 +1,7 @@
 """GPU parity tests for the dense path (sigmoid_attention -> myops::sigmoid_attention_fwd/bwd
 -> libsigattn.so).  Mirrors the reference's tests/test_sigmoid_dense.py."""
 
+import ctypes
 import math
 
 import numpy as np
@@ -12,6 +13,7 @@ from conftest import get_tolerance
 from helpers import (assert_close_to_oracle, assert_reference_criterion, criterion_errors,
                      oracle_fwd_bwd, randn)
 from oracle.eager import sigmoid_attention_eager
+from triton_sigmoid import _capi
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -246,6 +248,33 @@ def test_rows_off_16_byte_boundaries_match_oracle(dtype, causal):
     assert_close_to_oracle(q.grad, dq, dtype, "dQ")
     assert_close_to_oracle(k.grad, dk, dtype, "dK")
     assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
+@pytest.mark.parametrize("D,dtype", [(64, torch.float16), (32, torch.bfloat16), (16, torch.bfloat16)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_mod", [False, True])
+def test_one_launch_backward_equals_the_two_kernels(D, dtype, causal, with_mod):
+    """At c2's size (B=2 L=1024 H=8: 128 dQ and 128 dK/dV workgroups) the
+    recompute backward runs both kernels as one launch; its dQ, dK and dV
+    equal those of the two kernels run alone (sigattn_bwd_dq,
+    sigattn_bwd_dkdv) bit for bit."""
+    lib = _capi.load_library()
+    B, T, H = 2, 1024, 8
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=D + 2 * causal + with_mod)
+    bias = torch.full((B,), -math.log(T), device=DEV)
+    scale = torch.tensor(1 / math.sqrt(D), device=DEV)
+    sm = torch.randn((B, T), generator=torch.Generator().manual_seed(4)).to(DEV) if with_mod else None
+    pr = _capi._problem(q, k, v, bias, sm, scale, None, None, causal)
+    stream = torch.cuda.current_stream().cuda_stream
+    one = [torch.full_like(q, float("nan")) for _ in range(3)]
+    two = [torch.full_like(q, float("nan")) for _ in range(3)]
+    assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), *(t.data_ptr() for t in one), stream) == 0
+    assert lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), two[0].data_ptr(), stream) == 0
+    assert lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), two[1].data_ptr(), two[2].data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), one, two):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), name
 
 
 # --- behaviour -----------------------------------------------------------------

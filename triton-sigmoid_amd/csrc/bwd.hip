@@ -33,7 +33,7 @@ namespace sigattn {
 //   from the K tile with ds_read_b64_tr_b16.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
+__device__ __forceinline__ void bwd_dq_body(const KParams &p, const int wg) {
   constexpr int BM = 128, BN = 64;
   constexpr int NKS = D / 16, NDB = D / 32;
 
@@ -45,20 +45,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its keys
   if (!CAUSAL && p.rsplit > 1) {
     int bh;
-    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    ritem = wg / p.rsplit, rchunk = wg % p.rsplit;
     dense_item(ritem, p.B * p.H, p.nblk, true, bh, qb);
     b = bh / p.H, h = bh % p.H;
   } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
                                                      D <= 64 ? 3 : 2)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
+                               : WorkOrder::by_stream(wg, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb = it.blk;
   } else {
     const int BH = p.B * p.H;
     int bh;
-    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb);
+    dense_item(wg, BH, p.nblk, !CAUSAL, bh, qb);
     if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }
@@ -244,6 +244,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
   }
 }
 
+template <typename T, int D, bool CAUSAL, bool SCOREMOD>
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
+  bwd_dq_body<T, D, CAUSAL, SCOREMOD>(p, blockIdx.x);
+}
+
 // ---------------------------------------------------------------------------
 // dK/dV: workgroup = 4 waves x 32 keys (one wave per SIMD); the
 // queries stream through a 4-stage ring of 64-query Q and dO tiles as a
@@ -260,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
 // words of the few blocks that need them.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, bool SCOREMOD, bool DSOUT>
-__global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
+__device__ __forceinline__ void bwd_dkdv_body(const KParams &p, const int wg) {
   constexpr int BN = 128;                 // keys per workgroup (32 per wave)
   constexpr int BMQ = 64;                 // queries per LDS tile (two 32-query blocks)
   constexpr int NST = 4;                  // LDS ring stages
@@ -282,20 +287,20 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
   int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its queries
   if (!CAUSAL && !DSOUT && p.rsplit > 1) {
     int bh;
-    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    ritem = wg / p.rsplit, rchunk = wg % p.rsplit;
     dense_item(ritem, p.B * p.H, p.nblk, true, bh, kblk);
     b = bh / p.H, h = bh % p.H;
   } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lk, BN, p.nblk, false, p.ncu,
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lk, BN, p.nblk, false, p.ncu,
                                                      D <= 64 ? 2 : 1)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lk, BN, p.nblk, lq);
+                               : WorkOrder::by_stream(wg, p.B, p.H, lk, BN, p.nblk, lq);
     b = it.b, h = it.h, kblk = it.blk;
   } else {
     const int BH = p.B * p.H;
     int bh;
-    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, kblk);  // causal: low key blocks (the most work) first
+    dense_item(wg, BH, p.nblk, !CAUSAL, bh, kblk);  // causal: low key blocks (the most work) first
     b = bh / p.H, h = bh % p.H;
   }
   const int Lq = p.len_q(b);
@@ -607,6 +612,23 @@ __global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const 
       }
     }
   }
+}
+
+template <typename T, int D, bool CAUSAL, bool SCOREMOD, bool DSOUT>
+__global__ __launch_bounds__(256, (D <= 64 ? 2 : 1)) void bwd_dkdv_kernel(const KParams p) {
+  bwd_dkdv_body<T, D, CAUSAL, SCOREMOD, DSOUT>(p, blockIdx.x);
+}
+
+// The recompute backward's two kernels in one launch (dense problems at
+// D <= 64 whose two grids together need at most one workgroup per CU): the
+// first ndq workgroups run dQ items, the rest dK/dV items, so the two halves
+// share the GPU instead of each leaving half of it idle.  The bodies are the
+// kernels' own, so results are bit-identical to the two launches.  The two
+// bodies' LDS adds up (96 KB at D = 64), so one workgroup fits per CU.
+template <typename T, int D, bool CAUSAL, bool SCOREMOD>
+__global__ __launch_bounds__(256, 1) void bwd_fused_kernel(const KParams pq, const KParams pk, int ndq) {
+  if ((int)blockIdx.x < ndq) bwd_dq_body<T, D, CAUSAL, SCOREMOD>(pq, blockIdx.x);
+  else bwd_dkdv_body<T, D, CAUSAL, SCOREMOD, false>(pk, (int)blockIdx.x - ndq);
 }
 
 // ---------------------------------------------------------------------------
@@ -1365,6 +1387,28 @@ void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool 
     using T = std::remove_pointer_t<decltype(t)>;
     if (dsout) bwd_dkdv_t<T, decltype(d)::value, true>(p, causal, sm, st);
     else bwd_dkdv_t<T, decltype(d)::value, false>(p, causal, sm, st);
+  });
+}
+
+void launch_bwd_fused_mfma(const KParams &kp, int dtype, int D, bool causal, bool sm, hipStream_t st) {
+  by_type(dtype, D, [&](auto *t, auto d) {
+    using T = std::remove_pointer_t<decltype(t)>;
+    constexpr int DD = decltype(d)::value;
+    if constexpr (DD <= 64) {
+      KParams pq = kp, pk = kp;
+      pq.nblk = (kp.Tq + 127) / 128;
+      pk.nblk = (kp.Tk + 127) / 128;
+      pq.rsplit = pk.rsplit = 1;
+      const int ndq = pq.nblk * kp.B * kp.H;
+      const dim3 grid((unsigned)(ndq + pk.nblk * kp.B * kp.H));
+      if (causal) {
+        if (sm) bwd_fused_kernel<T, DD, true, true><<<grid, 256, 0, st>>>(pq, pk, ndq);
+        else bwd_fused_kernel<T, DD, true, false><<<grid, 256, 0, st>>>(pq, pk, ndq);
+      } else {
+        if (sm) bwd_fused_kernel<T, DD, false, true><<<grid, 256, 0, st>>>(pq, pk, ndq);
+        else bwd_fused_kernel<T, DD, false, false><<<grid, 256, 0, st>>>(pq, pk, ndq);
+      }
+    }
   });
 }
 

@@ -131,6 +131,18 @@ bool is_ragged(const sigattn_problem *p) {
          p->cu_seqlens_k != nullptr;
 }
 
+// The recompute backward's dQ and dK/dV kernels run as one launch
+// (launch_bwd_fused_mfma) when the problem is dense, its 16-bit kernel
+// instance has D <= 64, and the two grids (128 rows per workgroup) together
+// need at most one workgroup per CU: apart, each would leave the CUs the
+// other needs idle.
+bool fuse_backward(const sigattn_problem *p) {
+  if (is_ragged(p) || mfma_head_dim(p) > 64) return false;
+  const int64_t cus = sigattn::device_compute_units();
+  const int64_t wgs = p->B * p->H * (cdiv(p->Tq, 128) + cdiv(p->Tk, 128));
+  return cus > 0 && wgs <= cus;
+}
+
 // Fewest rows of the streamed range (keys for the forward and dQ kernels,
 // queries for dK/dV) that a range-split chunk takes; chunks of at least twice
 // as many may run two workgroups per CU.
@@ -525,6 +537,10 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   // the other: each fills the GPU on its own and they cannot share a CU
   // (their LDS footprints add up to more than one CU holds), so running them
   // concurrently on two streams only made both slower (measured).
+  if (need_dq && need_dkdv && mfma && fuse_backward(p)) {
+    sigattn::launch_bwd_fused_mfma(k, dt, D, causal, sm, st);
+    return launch_status();
+  }
   if (need_dq) {
     if (mfma) sigattn::launch_bwd_dq_mfma(k, dt, D, causal, sm, st);
     else if (f32mma) sigattn::launch_bwd_dq_f32(k, D, causal, sm, st);

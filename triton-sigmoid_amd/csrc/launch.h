@@ -36,6 +36,10 @@ void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool sc
                         hipStream_t st);
 void launch_bwd_dkdv_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
                           bool dsout, hipStream_t st);
+// Both recompute kernels in one launch: the first B·H·ceil(Tq/128)
+// workgroups run dQ items, the rest dK/dV items (dense problems, D <= 64;
+// bit-identical to launch_bwd_dq_mfma + launch_bwd_dkdv_mfma).
+void launch_bwd_fused_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod, hipStream_t st);
 // dQ = dS·K·scale from the dS tiles a launch_bwd_dkdv_mfma(dsout = true) on
 // the same problem stored in p.ds (two-pass backward).
 void launch_bwd_dq_ds_mfma(const KParams &p, int dtype, int D, bool causal, hipStream_t st);
