@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT / "triton-sigmoid_amd"))
 sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 MFMA (v_mfma_f32_32x32x2_f32)
 HBM_PEAK_TBPS = 8.0        # MI355X HBM3E
 METRIC = "fwd & fwd+bwd TFLOPS + % of fp16 MFMA peak, dense/padded L=4096 D=128"
 
@@ -57,7 +58,22 @@ CONFIGS = {
     # non-causal, through torch.compile(sigmoid_attention_padded).
     "c5": dict(B=4, L=8192, H=12, D=64, dtype="bfloat16", causal=False, padded=True, lo=1024,
                compiled=True),
+    # The other head dims and fp32 at the headline's shape (not BASELINE
+    # configs; they time the D = 32 instances, head_dim 16 inside them, and
+    # the fp32 MFMA kernels).
+    "d32": dict(B=4, L=4096, H=16, D=32, dtype="bfloat16", causal=True),
+    "d16": dict(B=4, L=4096, H=16, D=16, dtype="bfloat16", causal=True),
+    "f32": dict(B=4, L=4096, H=16, D=128, dtype="float32", causal=True),
+    "f32d64": dict(B=4, L=4096, H=16, D=64, dtype="float32", causal=True),
 }
+
+
+def peak_tflops(cfg) -> float:
+    """Dense MFMA peak of the config's dtype."""
+    return PEAK_F32_TFLOPS if cfg["dtype"] == "float32" else PEAK_BF16_TFLOPS
+
+
+DTYPE_LABEL = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}
 
 
 def log(*a):
@@ -703,24 +719,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if cfg["dtype"] == "bfloat16" else "fp16",
+        "dtype": DTYPE_LABEL[cfg["dtype"]],
         "data": "synthetic: q,k,v,dO ~ N(0,1) from torch.Generator seed 0",
         "config": {
             "workload": workload_name(args.config, cfg),
             "batch": B, "seq_len": L, "heads": H, "head_dim": D, "causal": causal,
         },
-        "pct_of_peak": round(100 * fb_tflops / PEAK_BF16_TFLOPS, 2),
+        "pct_of_peak": round(100 * fb_tflops / peak_tflops(cfg), 2),
         "fwd_tflops": round(res["fwd_tflops"], 2),
-        "fwd_pct_of_peak": round(100 * res["fwd_tflops"] / PEAK_BF16_TFLOPS, 2),
+        "fwd_pct_of_peak": round(100 * res["fwd_tflops"] / peak_tflops(cfg), 2),
         "bwd_only_tflops": round(10 * D * P / (bwd_ms * 1e-3) / 1e12, 2),
         "kernel_ms": {n: round(t, 4) for n, t in kt.items()},
         "roofline": {
             "kernel": dominant,
             "bound": "mfma",
             "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
+            "peak": peak_tflops(cfg),
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "frac": round(achieved / peak_tflops(cfg), 4),
             "traffic": load_traffic(dominant, args.config),
         },
         "cpu_baseline": cpu,
@@ -787,7 +803,7 @@ def measure_config(name: str, steps: int, warmup: int) -> dict:
     fb_tflops = fb_flops / (ms_step * 1e-3) / 1e12
     dominant = max(KERNELS, key=kt.get)
     log(f"[bench] config={name} {cfg}")
-    log(f"[bench] step {ms_step:.3f} ms -> fwd+bwd {fb_tflops:.1f} TFLOPS ({100 * fb_tflops / PEAK_BF16_TFLOPS:.1f}% peak)")
+    log(f"[bench] step {ms_step:.3f} ms -> fwd+bwd {fb_tflops:.1f} TFLOPS ({100 * fb_tflops / peak_tflops(cfg):.1f}% peak)")
     log(f"[bench] fwd {fwd_ms:.3f} ms -> {fwd_tflops:.1f} TFLOPS; kernels (ms): "
         + ", ".join(f"{n}={t:.3f}" for n, t in kt.items()))
     out = dict(cfg=cfg, pairs=P, ms_step=ms_step, fb_tflops=fb_tflops, fwd_tflops=fwd_tflops, kernel_ms=kt,

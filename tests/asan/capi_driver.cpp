@@ -14,12 +14,14 @@
 
 namespace {
 std::vector<std::string> g_calls;
+std::vector<sigattn::KParams> g_hist;  // parameters of each launch since the last calls()
 sigattn::KParams g_last{};
 int g_D = 0;  // head dim passed to the last kernel launch
 int g_fail = 0;
 
 void record(const char *name, const sigattn::KParams &p) {
   g_calls.emplace_back(name);
+  g_hist.push_back(p);
   g_last = p;
 }
 
@@ -53,6 +55,21 @@ std::string calls() {
   for (auto &c : g_calls) s += (s.empty() ? "" : ",") + c;
   g_calls.clear();
   return s;
+}
+
+// Launch i since the previous calls() zeroes gap rows in leading workgroups
+// (a multiple of 8 per axis): rq rows of the Q-shaped output q, rk rows of
+// the K-shaped outputs k0, k1 (0 rows: none for that axis).
+bool gaps_at(size_t i, int64_t rq, const void *q, int64_t rk = 0, const void *k0 = nullptr,
+             const void *k1 = nullptr) {
+  if (i >= g_hist.size()) return false;
+  const sigattn::KParams &k = g_hist[i];
+  const auto axis = [&](int a, int64_t rows, const void *o0, const void *o1) {
+    if (rows == 0) return k.ngap[a] == 0;
+    return k.gap[a].rows == rows && k.ngap[a] == (int)(((rows + 63) / 64 + 7) / 8 * 8) &&
+           k.gap[a].out[0] == o0 && k.gap[a].out[1] == o1;
+  };
+  return axis(0, rq, q, nullptr) && axis(1, rk, k0, k1);
 }
 }  // namespace
 
@@ -352,20 +369,55 @@ int main() {
     EXPECT(g_calls.empty());
   }
   {
-    // Packed layout: the rows outside every sequence are zeroed by one launch
-    // ahead of the attention kernels, for the outputs each call writes.
+    // Packed layout: the rows outside every sequence are zeroed by the
+    // leading workgroups of the MFMA forward (O) and dQ launch (dQ, and dK /
+    // dV too), or by a launch of their own on the portable kernels and when
+    // no such kernel runs.
     sigattn_problem p = base(3, 300, 2, 128);
     p.cu_seqlens_q = p.cu_seqlens_k = (const int32_t *)kFake;
     p.rows_q = 700, p.rows_k = 650;
     p.q_stride_b = p.k_stride_b = 0;
-    EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "zero_gaps,fwd_mfma");
-    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[0].T == 300 && sigattn::g_gap[0].out[0] == kFake &&
-           sigattn::g_gap[1].rows == 0);
-    EXPECT(sigattn_bwd(&p, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "zero_gaps,dq_mfma,dkdv_mfma");
-    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[1].rows == 650 && sigattn::g_gap[1].B == 3 &&
-           sigattn::g_gap[1].out[0] == kFake && sigattn::g_gap[1].out[1] == kFake);
-    EXPECT(sigattn_bwd_dkdv(&p, kFake, kFake, kFake, nullptr) == 0 && calls() == "zero_gaps,dkdv_mfma");
-    EXPECT(sigattn::g_gap[0].rows == 0 && sigattn::g_gap[1].rows == 650);
+    char *o = (char *)kFake, *dq = o + 4096, *dk = o + 8192, *dv = o + 12288;
+    g_hist.clear();
+    EXPECT(sigattn_fwd(&p, o, nullptr) == 0 && calls() == "fwd_mfma" && gaps_at(0, 700, o));
+    EXPECT(g_hist[0].gap[0].T == 300 && g_hist[0].gap[0].B == 3 && g_hist[0].gap[0].cu == kFake);
+    g_hist.clear();
+    EXPECT(sigattn_bwd(&p, kFake, dq, dk, dv, nullptr) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    EXPECT(gaps_at(0, 700, dq, 650, dk, dv) && gaps_at(1, 0, nullptr));
+    g_hist.clear();
+    EXPECT(sigattn_bwd_dq(&p, kFake, dq, nullptr) == 0 && calls() == "dq_mfma" && gaps_at(0, 700, dq));
+    // dK/dV alone: no dQ launch, so a launch of their own.
+    g_hist.clear();
+    EXPECT(sigattn_bwd_dkdv(&p, kFake, dk, dv, nullptr) == 0 && calls() == "zero_gaps,dkdv_mfma" &&
+           gaps_at(0, 0, nullptr));
+    EXPECT(sigattn::g_gap[0].rows == 0 && sigattn::g_gap[1].rows == 650 && sigattn::g_gap[1].out[0] == dk);
+    // Two-pass backward: the first head group's dQ-from-dS launch.
+    const size_t ws = sigattn_bwd_workspace_bytes(&p);
+    g_hist.clear();
+    EXPECT(sigattn_bwd_ws(&p, kFake, dq, dk, dv, kFake, ws, nullptr) == 0 && calls() == "dkdv_mfma_ds,dq_ds");
+    EXPECT(gaps_at(0, 0, nullptr) && gaps_at(1, 700, dq, 650, dk, dv));
+    g_hist.clear();
+    EXPECT(sigattn_bwd_ws(&p, kFake, dq, dk, dv, kFake, ws / 2, nullptr) == 0 &&
+           calls() == "dkdv_mfma_ds,dq_ds,dkdv_mfma_ds,dq_ds");
+    EXPECT(gaps_at(0, 0, nullptr) && gaps_at(1, 700, dq, 650, dk, dv) && gaps_at(2, 0, nullptr) &&
+           gaps_at(3, 0, nullptr));
+    // fp32: the fp32 MFMA kernels, likewise.
+    p.dtype = SIGATTN_F32;
+    g_hist.clear();
+    EXPECT(sigattn_fwd(&p, o, nullptr) == 0 && calls() == "fwd_f32" && gaps_at(0, 700, o));
+    g_hist.clear();
+    EXPECT(sigattn_bwd(&p, kFake, dq, dk, dv, nullptr) == 0 && calls() == "dq_f32,dkdv_f32" &&
+           gaps_at(0, 700, dq, 650, dk, dv) && gaps_at(1, 0, nullptr));
+    // Rows off 16-byte boundaries: the portable kernels and one gap launch.
+    p.q_stride_t = 2 * 128 + 2;
+    g_hist.clear();
+    EXPECT(sigattn_fwd(&p, o, nullptr) == 0 && calls() == "zero_gaps,fwd_generic");
+    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[0].out[0] == o && sigattn::g_gap[1].rows == 0);
+    EXPECT(sigattn_bwd(&p, kFake, dq, dk, dv, nullptr) == 0 && calls() == "zero_gaps,dq_generic,dkdv_generic");
+    EXPECT(sigattn::g_gap[0].rows == 700 && sigattn::g_gap[1].rows == 650 && sigattn::g_gap[1].out[0] == dk &&
+           sigattn::g_gap[1].out[1] == dv);
+    p.q_stride_t = 2 * 128;
+    p.dtype = SIGATTN_BF16;
     // No sequences (B = 0) or no queries: every row is a gap; none without rows.
     p.B = 0;
     EXPECT(sigattn_fwd(&p, kFake, nullptr) == 0 && calls() == "zero_gaps");

@@ -123,9 +123,10 @@ def test_varlen_many_sequences_and_zero_lengths():
                          _run_varlen(q, k, v, do, sq, sk, True), sq, sk, "B=80")
 
 
-def _packed_c_abi(q, k, v, do, cu, T, causal, fill):
+def _packed_c_abi(q, k, v, do, cu, T, causal, fill, two_pass=False, halves=False):
     """sigattn_fwd and sigattn_bwd on packed rows through the C ABI, with
-    every output pre-filled with `fill`."""
+    every output pre-filled with `fill`; two_pass: sigattn_bwd_ws with the
+    whole dS workspace; halves: sigattn_bwd_dkdv, then sigattn_bwd_dq."""
     lib = _capi.load_library()
     B = cu.numel() - 1
     lens = (cu[1:] - cu[:-1]).clamp(min=1).float()
@@ -135,8 +136,18 @@ def _packed_c_abi(q, k, v, do, cu, T, causal, fill):
     out, dq, dk, dv = (torch.full_like(q, fill) for _ in range(4))
     stream = torch.cuda.current_stream().cuda_stream
     assert lib.sigattn_fwd(ctypes.byref(pr), out.data_ptr(), stream) == 0
-    assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                           stream) == 0
+    if two_pass:
+        nbytes = lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))
+        assert nbytes > 0
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        assert lib.sigattn_bwd_ws(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                  ws.data_ptr(), nbytes, stream) == 0
+    elif halves:
+        assert lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), dk.data_ptr(), dv.data_ptr(), stream) == 0
+        assert lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), stream) == 0
+    else:
+        assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                               stream) == 0
     torch.cuda.synchronize()
     assert B >= 0
     return out, dq, dk, dv
@@ -163,6 +174,28 @@ def test_packed_rows_outside_sequences_are_zero(D, dtype, cu_rows, T, outside):
     ref = _packed_c_abi(q, k, v, do, cu, T, True, 0.0)
     mask = torch.zeros(rows, dtype=torch.bool, device=DEV)
     for a, b in outside:
+        mask[a:b] = True
+    for name, t, r in zip(("O", "dQ", "dK", "dV"), got, ref):
+        assert torch.all(t[mask] == 0), f"{name}: rows outside every sequence are not zero"
+        assert torch.all(torch.isfinite(t[~mask])), f"{name}: a sequence row is not finite"
+        assert torch.equal(t, r), f"{name}: differs from the run on zero-filled outputs"
+
+
+@pytest.mark.parametrize("how", ["two_pass", "halves"])
+def test_packed_gap_rows_other_backward_paths(how):
+    """The gap rows are zeroed on the backward's other routes too: the
+    two-pass backward (its first dQ-from-dS launch zeroes the dQ, dK and dV
+    gaps) and the halves called one by one (dK/dV alone zeroes its own by a
+    launch of its own)."""
+    H, D, rows, T = 2, 128, 700, 300
+    g = torch.Generator().manual_seed(10)
+    q, k, v, do = (randn((rows, H, D), torch.bfloat16, DEV, g) for _ in range(4))
+    cu = torch.tensor([40, 250, 250, 611], dtype=torch.int32, device=DEV)
+    kw = {how: True}
+    got = _packed_c_abi(q, k, v, do, cu, T, True, float("nan"), **kw)
+    ref = _packed_c_abi(q, k, v, do, cu, T, True, 0.0, **kw)
+    mask = torch.zeros(rows, dtype=torch.bool, device=DEV)
+    for a, b in [(0, 40), (550, 611), (611, 700)]:
         mask[a:b] = True
     for name, t, r in zip(("O", "dQ", "dK", "dV"), got, ref):
         assert torch.all(t[mask] == 0), f"{name}: rows outside every sequence are not zero"

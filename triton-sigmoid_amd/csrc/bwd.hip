@@ -246,7 +246,9 @@ __device__ __forceinline__ void bwd_dq_body(const KParams &p, const int wg) {
 
 template <typename T, int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const KParams p) {
-  bwd_dq_body<T, D, CAUSAL, SCOREMOD>(p, blockIdx.x);
+  __shared__ unsigned long long gap_lds[2];
+  const int wg = gap_prologue<2>(p, gap_lds);  // packed layouts: leading gap-zeroing workgroups
+  if (wg >= 0) bwd_dq_body<T, D, CAUSAL, SCOREMOD>(p, wg);
 }
 
 // ---------------------------------------------------------------------------
@@ -1085,17 +1087,19 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) 
   __shared__ __attribute__((aligned(16))) uint16_t sK[NST][BN * D];
   __shared__ __attribute__((aligned(16))) uint16_t sS[NST][NW * 2 * KB * TE];
 
+  const int wg = gap_prologue<2>(p, sK);  // packed layouts: leading gap-zeroing workgroups
+  if (wg < 0) return;
   int b, h, qblk;
   if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu, 1)
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu, 1)
+                               : WorkOrder::by_stream(wg, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qblk = it.blk;
   } else {
     const int BH = p.B * p.H;
     int bh;
-    dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qblk);
+    dense_item(wg, BH, p.nblk, !CAUSAL, bh, qblk);
     if (CAUSAL) qblk = p.nblk - 1 - qblk;  // heaviest query blocks first
     b = bh / p.H, h = bh % p.H;
   }
@@ -1282,6 +1286,7 @@ static void bwd_dq_t(const KParams &kp, bool causal, bool sm, hipStream_t st) {
   launch_rows<128>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
     // Range split (dense non-causal): rsplit workgroups per item.
     if (!causal && p.rsplit > 1) grid.x *= (unsigned)p.rsplit;
+    grid.x += (unsigned)(p.ngap[0] + p.ngap[1]);
     if (causal) {
       if (sm) bwd_dq_kernel<T, D, true, true><<<grid, 256, 0, st>>>(p);
       else bwd_dq_kernel<T, D, true, false><<<grid, 256, 0, st>>>(p);
@@ -1344,6 +1349,7 @@ static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
     // of a 4-wave workgroup; two waves per SIMD), one 32-key block per stage
     // in a 4-stage ring.  D = 64: 4 waves (the K rows of a 32-key stage do not
     // divide over 8 waves' copies), 6-stage ring.
+    grid.x += (unsigned)(p.ngap[0] + p.ngap[1]);
     if constexpr (D == 128) {
       if (causal) bwd_dq_ds_kernel<T, D, true, NW128, 1, NST128><<<grid, 64 * NW128, 0, st>>>(p);
       else bwd_dq_ds_kernel<T, D, false, NW128, 1, NST128><<<grid, 64 * NW128, 0, st>>>(p);
@@ -1399,6 +1405,7 @@ void launch_bwd_fused_mfma(const KParams &kp, int dtype, int D, bool causal, boo
       pq.nblk = (kp.Tq + 127) / 128;
       pk.nblk = (kp.Tk + 127) / 128;
       pq.rsplit = pk.rsplit = 1;
+      pq.ngap[0] = pq.ngap[1] = pk.ngap[0] = pk.ngap[1] = 0;  // dense problems only: no packed gap rows
       const int ndq = pq.nblk * kp.B * kp.H;
       const dim3 grid((unsigned)(ndq + pk.nblk * kp.B * kp.H));
       if (causal) {

@@ -276,9 +276,12 @@ KParams head_slice(const KParams &k, int64_t h0, int64_t nh, int64_t esize) {
 // Tq / Tk of a longer one), so every row of a packed output is written.
 // q_out is the Q-shaped output (O or dQ), k_out0 / k_out1 the K-shaped ones
 // (dK, dV); nullptr skips a tensor.  One launch for both axes, on `st`.
-void zero_packed_gaps(const sigattn_problem *p, void *q_out, void *k_out0, void *k_out1, hipStream_t st) {
+// The packed axes whose output rows outside every sequence must be zeroed:
+// a for the Q-shaped output, b for the K-shaped ones (rows = 0: none).
+void gap_axes(const sigattn_problem *p, void *q_out, void *k_out0, void *k_out1, sigattn::GapAxis &a,
+              sigattn::GapAxis &b) {
+  a = b = sigattn::GapAxis{};
   if (p->H == 0) return;
-  sigattn::GapAxis a, b;
   if (p->cu_seqlens_q != nullptr && q_out != nullptr && p->rows_q > 0) {
     a.cu = p->cu_seqlens_q;
     a.B = (int)p->B, a.T = (int)p->Tq, a.H = (int)p->H, a.D = (int)p->D;
@@ -291,7 +294,25 @@ void zero_packed_gaps(const sigattn_problem *p, void *q_out, void *k_out0, void 
     b.rows = p->rows_k, b.st = p->k_stride_t, b.sh = p->k_stride_h;
     b.out[0] = k_out0, b.out[1] = k_out1;
   }
+}
+
+// Zeroes those rows with a launch of their own (paths whose kernels do not
+// take KParams::gap, and calls that launch no attention kernel).
+void zero_packed_gaps(const sigattn_problem *p, void *q_out, void *k_out0, void *k_out1, hipStream_t st) {
+  sigattn::GapAxis a, b;
+  gap_axes(p, q_out, k_out0, k_out1, a, b);
   sigattn::launch_zero_gaps(a, b, p->dtype == SIGATTN_F32 ? 4 : 2, st);
+}
+
+// Hands axes a and b to the kernel launched with `k` (a forward or dQ
+// kernel): its first workgroups, a multiple of 8 per axis, zero the axes'
+// gap rows (KParams::gap).
+void use_gaps(KParams &k, const sigattn::GapAxis &a, const sigattn::GapAxis &b) {
+  const sigattn::GapAxis *ax[2] = {&a, &b};
+  for (int i = 0; i < 2; ++i) {
+    k.gap[i] = *ax[i];
+    k.ngap[i] = ax[i]->rows > 0 ? (int)(cdiv(cdiv(ax[i]->rows, 64), 8) * 8) : 0;
+  }
 }
 
 int launch_status() {
@@ -429,7 +450,16 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     if (rs.n > 1 && ((size_t)rs.bytes > workspace_bytes || !aligned16(workspace))) rs = RangeSplit{};
   }
   (void)hipGetLastError();
-  zero_packed_gaps(p, out, nullptr, nullptr, st);
+  // Packed rows outside every sequence: zeroed by the MFMA forward's leading
+  // workgroups, by a launch of their own on the other paths.
+  const bool f32mma = use_f32_mfma(p, ptrs, 4);
+  if (sp.nsplit == 0 && (mfma || f32mma)) {
+    sigattn::GapAxis gq, gk;
+    gap_axes(p, out, nullptr, nullptr, gq, gk);
+    use_gaps(k, gq, gk);
+  } else {
+    zero_packed_gaps(p, out, nullptr, nullptr, st);
+  }
   if (rs.n > 1) {
     use_range_split(k, rs, workspace);
     sigattn::launch_rs_clear(k.rs_cnt, (int)rs.items, nullptr, 0, st);
@@ -440,7 +470,7 @@ static int fwd_impl(const sigattn_problem *p, void *out, void *workspace, size_t
     sigattn::launch_fwd_splitkv(k, p->dtype, (int)p->D, p->score_mod != nullptr, st);
   } else if (mfma) {
     sigattn::launch_fwd_mfma(k, p->dtype, mfma_head_dim(p), p->causal != 0, p->score_mod != nullptr, st);
-  } else if (use_f32_mfma(p, ptrs, 4)) {
+  } else if (f32mma) {
     sigattn::launch_fwd_f32(k, mfma_head_dim(p), p->causal != 0, p->score_mod != nullptr, st);
   } else {
     sigattn::launch_fwd_generic(k, p->dtype, (int)p->D, p->causal != 0, st);
@@ -516,8 +546,16 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
   const bool causal = p->causal != 0, sm = p->score_mod != nullptr;
   const int dt = p->dtype, D = mfma || f32mma ? mfma_head_dim(p) : (int)p->D;
   (void)hipGetLastError();
-  zero_packed_gaps(p, parts != kBwdDkdv ? dq : nullptr, parts != kBwdDq ? dk : nullptr,
-                   parts != kBwdDq ? dv : nullptr, st);
+  // Packed rows outside every sequence: zeroed, for dQ and dK / dV alike, by
+  // the leading workgroups of the MFMA dQ launch (whose kernels have the
+  // registers to spare; in the dK/dV kernel at D = 64 the extra code path
+  // pushed spills into the main loop), by a launch of their own when the
+  // portable kernels run or no dQ kernel does.
+  sigattn::GapAxis gq, gk;
+  gap_axes(p, parts != kBwdDkdv ? dq : nullptr, parts != kBwdDq ? dk : nullptr, parts != kBwdDq ? dv : nullptr, gq,
+           gk);
+  const bool dq_gaps = (mfma || f32mma) && need_dq;
+  if (!dq_gaps) sigattn::launch_zero_gaps(gq, gk, dt == SIGATTN_F32 ? 4 : 2, st);
   if (twopass) {
     k.ds = (uint16_t *)workspace;
     k.ds_nqb = (int)cdiv(p->Tq, 32);
@@ -527,8 +565,9 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
     // group's dQ has read it.
     for (int64_t h0 = 0; h0 < p->H; h0 += heads_per_pass) {
       const int64_t nh = p->H - h0 < heads_per_pass ? p->H - h0 : heads_per_pass;
-      const KParams s = head_slice(k, h0, nh, 2);
+      KParams s = head_slice(k, h0, nh, 2);
       if (parts != kBwdDq) sigattn::launch_bwd_dkdv_mfma(s, dt, D, causal, sm, true, st);
+      if (h0 == 0 && dq_gaps) use_gaps(s, gq, gk);  // the first group's dQ launch
       if (parts != kBwdDkdv) sigattn::launch_bwd_dq_ds_mfma(s, dt, D, causal, st);
     }
     return launch_status();
@@ -541,9 +580,11 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
     sigattn::launch_bwd_fused_mfma(k, dt, D, causal, sm, st);
     return launch_status();
   }
+  KParams kq = k;
+  if (dq_gaps) use_gaps(kq, gq, gk);
   if (need_dq) {
-    if (mfma) sigattn::launch_bwd_dq_mfma(k, dt, D, causal, sm, st);
-    else if (f32mma) sigattn::launch_bwd_dq_f32(k, D, causal, sm, st);
+    if (mfma) sigattn::launch_bwd_dq_mfma(kq, dt, D, causal, sm, st);
+    else if (f32mma) sigattn::launch_bwd_dq_f32(kq, D, causal, sm, st);
     else sigattn::launch_bwd_dq_generic(k, dt, D, causal, st);
   }
   if (need_dkdv) {

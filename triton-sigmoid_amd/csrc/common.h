@@ -61,6 +61,17 @@ __device__ __forceinline__ int packed_len(const int32_t *cu, int64_t rows, int b
   return (int)(e - s < T ? e - s : T);
 }
 
+// One packed sequence axis whose output rows outside every sequence are to
+// be zeroed: cu_seqlens [B + 1], the axis's row count, its longest sequence
+// T, the outputs' row and head strides (elements) and up to two output
+// tensors (nullptr: none).  See zero_gap_rows.
+struct GapAxis {
+  const int32_t *cu = nullptr;
+  int B = 0, T = 0, H = 0, D = 0;
+  int64_t rows = 0, st = 0, sh = 0;
+  void *out[2] = {nullptr, nullptr};
+};
+
 // Kernel parameters (passed by value).  Strides are in elements.
 //
 // Each sequence axis (queries, keys) has one of three layouts:
@@ -102,6 +113,12 @@ struct KParams {
   float *rs_part;
   int *rs_cnt;
   int ncu;  // compute units of the device (WorkOrder::by_level's dealing rounds)
+  // Packed layouts: the first ngap[0] workgroups of the launch zero the rows
+  // of gap[0]'s outputs that no sequence covers (zero_gap_rows), the next
+  // ngap[1] those of gap[1], and do nothing else; the kernel's work items
+  // follow (gap_prologue).  0: none.
+  GapAxis gap[2];
+  int ngap[2];
   // Head dim of the tensors.  The D = 32 kernels also take head_dim 16
   // (dmem = 16): the stationary rows' upper 16 columns enter as zeros, the
   // streamed tiles repeat the 16 columns there (so every product over the
@@ -149,6 +166,80 @@ struct KParams {
     return cu_k == nullptr && sk_h == D && sk_t == (int64_t)H * D;
   }
 };
+
+// Zeroes the rows blk*64 .. blk*64+63 of `ax`'s outputs that no sequence
+// covers (256 threads): 64 threads find whether their row lies in a
+// sequence -- a binary search over cu when cu is non-decreasing (the
+// workgroup checks first), else a scan over every sequence -- and the
+// workgroup zeroes the uncovered rows' H x D elements.  Rows a sequence
+// covers are never written, so this may run in any order with the
+// attention work that writes them.  `lds`: 16 bytes of LDS (8-byte aligned)
+// the workgroup may use -- a kernel's own tile memory, which its gap
+// workgroups never touch otherwise.
+template <int ESIZE> __device__ __forceinline__ void zero_gap_rows(const GapAxis &ax, int blk, void *lds) {
+  const int64_t r0 = (int64_t)blk * 64;
+  unsigned long long &gaps = ((unsigned long long *)lds)[0];
+  int &sorted = ((int *)lds)[2];
+  if (threadIdx.x == 0) {
+    sorted = 1;
+    gaps = 0ull;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < ax.B; b += blockDim.x)
+    if (ax.cu[b + 1] < ax.cu[b]) sorted = 0;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int64_t r = r0 + threadIdx.x;
+    bool covered = false;
+    if (r < ax.rows && ax.B > 0) {
+      auto covers = [&](int b) {
+        const int64_t f = packed_first(ax.cu, ax.rows, b);
+        return r >= f && r < f + packed_len(ax.cu, ax.rows, b, ax.T);
+      };
+      if (sorted) {
+        // Largest b with first(b) <= r (first() is non-decreasing here).
+        int lo = 0, hi = ax.B - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) / 2;
+          if (packed_first(ax.cu, ax.rows, mid) <= r) lo = mid;
+          else hi = mid - 1;
+        }
+        covered = covers(lo);
+      } else {
+        for (int b = 0; b < ax.B && !covered; ++b) covered = covers(b);
+      }
+    }
+    const unsigned long long m = __ballot(r < ax.rows && !covered);
+    if (threadIdx.x == 0) gaps = m;
+  }
+  __syncthreads();
+  unsigned long long m = gaps;
+  const int per_row = ax.H * ax.D;
+  typedef typename std::conditional<ESIZE == 4, uint32_t, uint16_t>::type E;
+  while (m != 0ull) {
+    const int i = __builtin_ctzll(m);
+    m &= m - 1;
+    const int64_t row = (r0 + i) * ax.st;
+    for (int e = threadIdx.x; e < per_row; e += blockDim.x) {
+      const int h = e / ax.D, d = e - h * ax.D;
+      const int64_t off = row + (int64_t)h * ax.sh + d;
+      for (int t = 0; t < 2; ++t)
+        if (ax.out[t] != nullptr) ((E *)ax.out[t])[off] = (E)0;
+    }
+  }
+}
+
+// Work-item id of this workgroup, or -1 for the leading ngap[0] + ngap[1]
+// workgroups, which zero the gap rows of KParams::gap (ESIZE-byte elements)
+// instead.  Both counts are multiples of 8, so the items keep the XCD each
+// would have without them.
+template <int ESIZE> __device__ __forceinline__ int gap_prologue(const KParams &p, void *lds) {
+  const int id = (int)blockIdx.x;
+  if (id >= p.ngap[0] + p.ngap[1]) return id - p.ngap[0] - p.ngap[1];
+  if (id < p.ngap[0]) zero_gap_rows<ESIZE>(p.gap[0], id, lds);
+  else zero_gap_rows<ESIZE>(p.gap[1], id - p.ngap[0], lds);
+  return -1;
+}
 
 // Zero rows of the padded layout.  A row block wholly past a batch's valid
 // length is a padding work item for each of the H heads; when every head's

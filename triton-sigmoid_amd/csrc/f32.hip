@@ -106,9 +106,11 @@ __global__ __launch_bounds__(64 * FW, fwd_f32_occupancy<D>()) void fwd_f32_kerne
   __shared__ __attribute__((aligned(16))) float sV[2][FB * D];
   __shared__ float sC[SCOREMOD ? 2 : 1][FB];
 
+  const int wg = gap_prologue<4>(p, sK);  // packed layouts: leading gap-zeroing workgroups
+  if (wg < 0) return;
   const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  int qb = blockIdx.x / BH;
+  const int bh = wg % BH;
+  int qb = wg / BH;
   if (CAUSAL) qb = p.nblk - 1 - qb;  // heaviest query blocks first
   const int b = bh / p.H, h = bh % p.H;
   const int Lq = p.len_q(b), Lk = p.len_k(b);
@@ -195,9 +197,11 @@ __global__ __launch_bounds__(64 * FW, bwd_f32_occupancy<D>()) void dq_f32_kernel
   __shared__ __attribute__((aligned(16))) float sV[2][FB * D];
   __shared__ float sC[SCOREMOD ? 2 : 1][FB];
 
+  const int wg = gap_prologue<4>(p, sK);  // packed layouts: leading gap-zeroing workgroups
+  if (wg < 0) return;
   const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  int qb = blockIdx.x / BH;
+  const int bh = wg % BH;
+  int qb = wg / BH;
   if (CAUSAL) qb = p.nblk - 1 - qb;
   const int b = bh / p.H, h = bh % p.H;
   const int Lq = p.len_q(b), Lk = p.len_k(b);
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(64 * FW, bwd_f32_occupancy<D>()) void dkdv_f32_kern
 template <int D> void fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
   KParams p = kp;
   p.nblk = (p.Tq + FBM - 1) / FBM;
-  const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(64 * FW);
+  const dim3 grid((unsigned)(p.nblk * p.B * p.H + p.ngap[0] + p.ngap[1])), block(64 * FW);
   if (causal) {
     if (scoremod) fwd_f32_kernel<D, true, true><<<grid, block, 0, st>>>(p);
     else fwd_f32_kernel<D, true, false><<<grid, block, 0, st>>>(p);
@@ -386,7 +390,7 @@ template <int D> void fwd_t(const KParams &kp, bool causal, bool scoremod, hipSt
 template <int D> void dq_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
   KParams p = kp;
   p.nblk = (p.Tq + FBM - 1) / FBM;
-  const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(64 * FW);
+  const dim3 grid((unsigned)(p.nblk * p.B * p.H + p.ngap[0] + p.ngap[1])), block(64 * FW);
   if (causal) {
     if (scoremod) dq_f32_kernel<D, true, true><<<grid, block, 0, st>>>(p);
     else dq_f32_kernel<D, true, false><<<grid, block, 0, st>>>(p);
@@ -399,7 +403,7 @@ template <int D> void dq_t(const KParams &kp, bool causal, bool scoremod, hipStr
 template <int D> void dkdv_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
   KParams p = kp;
   p.nblk = (p.Tk + FBM - 1) / FBM;
-  const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(64 * FW);
+  const dim3 grid((unsigned)(p.nblk * p.B * p.H)), block(64 * FW);  // no gap rows here (the dQ launch's)
   if (causal) {
     if (scoremod) dkdv_f32_kernel<D, true, true><<<grid, block, 0, st>>>(p);
     else dkdv_f32_kernel<D, true, false><<<grid, block, 0, st>>>(p);

@@ -91,20 +91,22 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sV[NST][BN * D];
   __shared__ __attribute__((aligned(16))) float sC[SCOREMOD ? NST * BN : 4];
 
+  const int wg = gap_prologue<2>(p, sK);  // packed layouts: leading gap-zeroing workgroups
+  if (wg < 0) return;
   int b, h, qb0, nitems = 1;
   int ritem = 0, rchunk = 0;  // range split: the item and this workgroup's chunk of its keys
   if (!CAUSAL && p.rsplit > 1) {
     // Small dense grids: the rsplit workgroups of an item take adjacent ids.
     int bh;
-    ritem = blockIdx.x / p.rsplit, rchunk = blockIdx.x % p.rsplit;
+    ritem = wg / p.rsplit, rchunk = wg % p.rsplit;
     dense_item(ritem, p.B * p.H, p.nblk, true, bh, qb0);
     b = bh / p.H, h = bh % p.H;
   } else if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(blockIdx.x, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
                                                      fwd_occupancy<D>())
-                               : WorkOrder::by_stream(blockIdx.x, p.B, p.H, lq, BM, p.nblk, lk);
+                               : WorkOrder::by_stream(wg, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb0 = it.blk;
   } else {
     const int BH = p.B * p.H;
@@ -116,18 +118,18 @@ __global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(
       // the XCD-grouped order (K and V of a (batch, head) read by its
       // workgroups while they sit in one L2) costs no balance.
       int j;
-      dense_item(blockIdx.x, BH, (p.nblk + 1) / 2, true, bh, j);
+      dense_item(wg, BH, (p.nblk + 1) / 2, true, bh, j);
       qb0 = p.nblk - 1 - j;
       nitems = j < qb0 ? 2 : 1;
     } else if (CAUSAL && D == 128 && kFwdBhGroup > 0 && BH % kFwdBhGroup == 0) {
       // Heaviest query blocks first within groups of kFwdBhGroup (batch,
       // head) pairs, group after group: each XCD (id % 8) holds the K / V
       // rows of kFwdBhGroup / 8 pairs at a time.
-      const int g = blockIdx.x / (kFwdBhGroup * p.nblk), r = blockIdx.x % (kFwdBhGroup * p.nblk);
+      const int g = wg / (kFwdBhGroup * p.nblk), r = wg % (kFwdBhGroup * p.nblk);
       bh = g * kFwdBhGroup + r % kFwdBhGroup;
       qb0 = p.nblk - 1 - r / kFwdBhGroup;
     } else {
-      dense_item(blockIdx.x, BH, p.nblk, !CAUSAL, bh, qb0);
+      dense_item(wg, BH, p.nblk, !CAUSAL, bh, qb0);
       if (CAUSAL) qb0 = p.nblk - 1 - qb0;  // heaviest query blocks first
     }
     b = bh / p.H, h = bh % p.H;
@@ -472,7 +474,7 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
   // two query blocks per workgroup.
   const bool pairs = causal && kFwdCausalPairs && !(p.ragged() && p.B <= 64);
   if (causal || p.rsplit < 1) p.rsplit = 1;
-  const dim3 grid((unsigned)((pairs ? (p.nblk + 1) / 2 : p.nblk) * p.B * p.H * p.rsplit));
+  const dim3 grid((unsigned)((pairs ? (p.nblk + 1) / 2 : p.nblk) * p.B * p.H * p.rsplit + p.ngap[0] + p.ngap[1]));
   const dim3 block(64 * NWV);
   if (causal) {
     if (scoremod) fwd_mfma_kernel<T, D, NWV, NCB, true, true><<<grid, block, 0, st>>>(p);

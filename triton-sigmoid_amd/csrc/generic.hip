@@ -245,73 +245,13 @@ SIGATTN_GENERIC_LAUNCHER(launch_bwd_dkdv_generic, dkdv_generic_kernel, p.Tk)
 
 #undef SIGATTN_GENERIC_LAUNCHER
 
-// ---- rows of packed outputs outside every sequence ------------------------------
-//
-// Sequence b of a packed axis covers rows packed_first(b) .. packed_first(b) +
-// packed_len(b) - 1 (cu_seqlens clamped to the rows, at most T rows); the
-// attention kernels write exactly those rows.  This kernel writes zeros to
-// every other row of the axis's output tensors (rows before cu[0], past
-// cu[B], past T rows of a longer sequence), so no output row is left
-// uninitialised.  Workgroup = 64 rows: lane i of the first wave decides row
-// r0 + i (a binary search over cu when cu is non-decreasing, which the
-// workgroup checks first, else a scan over every sequence), then the 256
-// threads zero the uncovered rows' H x D elements.  Rows a sequence covers are
-// never written, so the launch may run in either order with the attention
-// kernels.
+// Rows of packed outputs that no sequence covers, for two axes in one launch
+// (zero_gap_rows; the first nblk0 workgroups take ax0).
 template <int ESIZE>
 __global__ __launch_bounds__(256) void zero_gaps_kernel(const GapAxis ax0, const GapAxis ax1, int nblk0) {
+  __shared__ unsigned long long lds[2];
   const bool second = (int)blockIdx.x >= nblk0;
-  const GapAxis &ax = second ? ax1 : ax0;
-  const int64_t r0 = (int64_t)(second ? blockIdx.x - nblk0 : blockIdx.x) * 64;
-  __shared__ int sorted;
-  __shared__ unsigned long long gaps;
-  if (threadIdx.x == 0) {
-    sorted = 1;
-    gaps = 0ull;
-  }
-  __syncthreads();
-  for (int b = threadIdx.x; b < ax.B; b += 256)
-    if (ax.cu[b + 1] < ax.cu[b]) sorted = 0;
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int64_t r = r0 + threadIdx.x;
-    bool covered = false;
-    if (r < ax.rows && ax.B > 0) {
-      auto covers = [&](int b) {
-        const int64_t f = packed_first(ax.cu, ax.rows, b);
-        return r >= f && r < f + packed_len(ax.cu, ax.rows, b, ax.T);
-      };
-      if (sorted) {
-        // Largest b with first(b) <= r (first() is non-decreasing here).
-        int lo = 0, hi = ax.B - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) / 2;
-          if (packed_first(ax.cu, ax.rows, mid) <= r) lo = mid;
-          else hi = mid - 1;
-        }
-        covered = covers(lo);
-      } else {
-        for (int b = 0; b < ax.B && !covered; ++b) covered = covers(b);
-      }
-    }
-    const unsigned long long m = __ballot(r < ax.rows && !covered);
-    if (threadIdx.x == 0) gaps = m;
-  }
-  __syncthreads();
-  unsigned long long m = gaps;
-  const int per_row = ax.H * ax.D;
-  typedef typename std::conditional<ESIZE == 4, uint32_t, uint16_t>::type E;
-  while (m != 0ull) {
-    const int i = __builtin_ctzll(m);
-    m &= m - 1;
-    const int64_t row = (r0 + i) * ax.st;
-    for (int e = threadIdx.x; e < per_row; e += 256) {
-      const int h = e / ax.D, d = e - h * ax.D;
-      const int64_t off = row + (int64_t)h * ax.sh + d;
-      for (int t = 0; t < 2; ++t)
-        if (ax.out[t] != nullptr) ((E *)ax.out[t])[off] = (E)0;
-    }
-  }
+  zero_gap_rows<ESIZE>(second ? ax1 : ax0, second ? (int)blockIdx.x - nblk0 : (int)blockIdx.x, lds);
 }
 
 void launch_zero_gaps(const GapAxis &a, const GapAxis &b, int esize, hipStream_t st) {

@@ -29,7 +29,11 @@ int bwd_dkdv_workgroups_per_cu(int D);
 // one launch on `st` (a kernel: no memset node lands in a captured graph).
 void launch_rs_clear(int *a, int na, int *b, int nb, hipStream_t st);
 
-// MFMA kernels: dtype in {kF16, kBF16}, D in {64, 128}, 16-byte aligned rows.
+// MFMA kernels: dtype in {kF16, kBF16}, D in {32, 64, 128} (head_dim 16 as
+// D = 32 with KParams::dmem = 16), 16-byte aligned rows.  The forward, dQ
+// and dQ-from-dS launches (and the fp32 forward and dQ below) also run
+// KParams::ngap leading workgroups that zero packed gap rows; the dK/dV
+// launches take none.
 void launch_fwd_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
                      hipStream_t st);
 void launch_bwd_dq_mfma(const KParams &p, int dtype, int D, bool causal, bool scoremod,
@@ -60,15 +64,6 @@ constexpr size_t kSplitScratchBytes = size_t(16) << 20;
 // device with hipGetSymbolAddress); hipSuccess or the lookup's error.
 hipError_t splitkv_scratch(float **ptr);
 
-// One packed sequence axis for launch_zero_gaps: cu_seqlens [B + 1], the
-// axis's row count, its longest sequence T, the outputs' row and head strides
-// (elements) and up to two output tensors (nullptr: none).
-struct GapAxis {
-  const int32_t *cu = nullptr;
-  int B = 0, T = 0, H = 0, D = 0;
-  int64_t rows = 0, st = 0, sh = 0;
-  void *out[2] = {nullptr, nullptr};
-};
 // Zeroes the rows of packed outputs that no sequence covers, for two axes in
 // one launch (an axis with rows = 0 takes no workgroups); esize = 2 or 4.
 void launch_zero_gaps(const GapAxis &a, const GapAxis &b, int esize, hipStream_t st);
