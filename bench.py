@@ -390,6 +390,9 @@ def traffic_json(config: str, fetch_csv: str, write_csv: str, cal_fetch_csv: str
     ds_bytes = B * H * ds_tiles * 2048 if D == 128 else 0
     algo = {"fwd": 4 * tensor, "bwd_dkdv": 6 * tensor + ds_bytes,
             "bwd_dq": (2 * tensor + ds_bytes) if ds_bytes else 5 * tensor}
+    # Without the two-pass backward's dS stream (written by dK/dV, read back
+    # by dQ): only the operator's own tensors each kernel reads or writes.
+    compulsory = {"fwd": 4 * tensor, "bwd_dkdv": 6 * tensor, "bwd_dq": 2 * tensor if ds_bytes else 5 * tensor}
     out = {"src_digest": kernel_source_digest(), "config": config,
            "calibration": {"copy_bytes": int(one_gib), "fetch_kib": fcal, "write_kib": wcal,
                            "fetch_factor": round(ffac, 4), "write_factor": round(wfac, 4)}}
@@ -404,7 +407,9 @@ def traffic_json(config: str, fetch_csv: str, write_csv: str, cal_fetch_csv: str
         nbytes = fk * 1024 * ffac + wk * 1024 * wfac
         entry[name] = {"kernel": _kernel_base(fks[0][0]), "bytes_per_launch": int(nbytes),
                        "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
-                       "algorithmic_bytes": int(algo[name]), "ratio": round(nbytes / algo[name], 3)}
+                       "algorithmic_bytes": int(algo[name]), "ratio": round(nbytes / algo[name], 3),
+                       "compulsory_bytes": int(compulsory[name]),
+                       "ratio_to_compulsory": round(nbytes / compulsory[name], 3)}
     out[config] = entry
     return out
 

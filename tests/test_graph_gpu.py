@@ -27,13 +27,31 @@ def _case(kind):
         B, T, H, D, dtype = 1, 2100, 2, 64, torch.float16
         q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
         return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v)
+    if kind == "dense_d64_one_launch_bwd":
+        # c2's causal shape: the backward's two kernels as one launch.
+        B, T, H, D, dtype = 2, 1024, 8, 64, torch.float16
+        q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
+        return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v, is_causal=True)
+    if kind == "fp32_d128":
+        B, T, H, D, dtype = 1, 300, 2, 128, torch.float32
+        q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
+        return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention(q, k, v, is_causal=True)
+    if kind == "packed_d64_gaps":
+        # Rows 510-570 lie past max_seqlen 300 of the 361-row sequence and
+        # rows 571-639 past cu[B]: the launches' leading workgroups zero them.
+        rows, H, D, dtype = 640, 2, 64, torch.float16
+        q, k, v, do = (randn((rows, H, D), dtype, DEV, g) for _ in range(4))
+        cu = torch.tensor([0, 210, 210, 571], dtype=torch.int32, device=DEV)
+        return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention_varlen(q, k, v, cu, cu, 300, 300,
+                                                                           is_causal=True)
     B, T, H, D, dtype = 3, 200, 2, 64, torch.float16
     q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
     sl = torch.tensor([200, 77, 130], dtype=torch.int32, device=DEV)
     return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl)
 
 
-@pytest.mark.parametrize("kind", ["dense_d128_causal", "dense_d64_range_split", "padded_d64"])
+@pytest.mark.parametrize("kind", ["dense_d128_causal", "dense_d64_range_split", "padded_d64",
+                                  "dense_d64_one_launch_bwd", "fp32_d128", "packed_d64_gaps"])
 def test_graph_replays_match_eager(kind):
     (q, k, v, do), attn = _case(kind)
     leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
