@@ -13,8 +13,11 @@
 // SIMD's cycles per instruction, a 32x32 block costs D instructions per
 // product pair against a few hundred cycles of sigmoid arithmetic, so these
 // kernels are plain: four waves of 32 stationary rows, streamed rows in a
-// two-stage ring of 32-row tiles copied straight into LDS, one barrier per
-// tile, no software pipeline.
+// ring of 32-row tiles copied straight into LDS, one barrier per tile.  Where
+// two or more waves share a SIMD, one wave's sigmoid arithmetic runs under
+// another's MFMAs; the backward kernels also spread it over their dP chains
+// (head_product_with), and at D = 128, one wave per SIMD, the dQ kernel runs
+// tile t's arithmetic under tile t+1's chains.
 //
 // Products over the head dim (S, dP) reduce d = s (lanes 0-31) and
 // d = D/2 + s (lanes 32-63) in step s, so four consecutive steps take one
@@ -93,9 +96,46 @@ __device__ __forceinline__ void store_row(float *row, const f32x16 (&acc)[D / 32
 }
 
 // Resident waves per SIMD (four-wave workgroups): registers bound them; the
-// LDS ring (2 stages x 2 tiles x 32 rows x D floats: 64 KB at D = 128) fits.
+// LDS ring (stages x 2 tiles x 32 rows x D floats: 64 KB at D = 128 with two
+// stages, 96 KB with three) fits.
 template <int D> constexpr int fwd_f32_occupancy() { return D == 128 ? 2 : (D == 64 ? 3 : 4); }
 template <int D> constexpr int bwd_f32_occupancy() { return D == 128 ? 1 : (D == 64 ? 2 : 3); }
+
+// Ring stages of the dQ kernel: three where one wave holds a SIMD (D = 128),
+// so that tile t+1's chains run while tile t's sigmoid arithmetic issues,
+// else two.
+#ifndef SIGATTN_F32_DQ_PIPE
+#define SIGATTN_F32_DQ_PIPE 1
+#endif
+template <int D> constexpr int dq_f32_stages() {
+  return SIGATTN_F32_DQ_PIPE && bwd_f32_occupancy<D>() == 1 ? 3 : 2;
+}
+
+// head_product with elem(i), i = 0..15 (a tile's per-element sigmoid
+// arithmetic), spread over the chain's pieces: a scheduling fence after each
+// piece keeps that VALU work between the MFMAs -- left to itself the compiler
+// places it after the last one, where a wave alone on its SIMD leaves the
+// matrix core idle.  Piece c+1's operand is read before piece c's MFMAs.
+template <int D, class Elem>
+__device__ __forceinline__ void head_product_with(f32x16 &acc, const float *t, const float (&v)[D / 2], int l32,
+                                                  int hi, Elem &&elem) {
+  constexpr int NP = D / 8, EPP = 16 / NP;
+  static_assert(NP * EPP == 16, "elements per piece");
+  f32x4 a = *(const f32x4 *)(t + F32Tile<D>::piece(l32, hi * NP));
+#pragma unroll
+  for (int c = 0; c < NP; ++c) {
+    f32x4 an = a;
+    if (c + 1 < NP) an = *(const f32x4 *)(t + F32Tile<D>::piece(l32, hi * NP + c + 1));
+    acc = mma(a.x, v[4 * c], acc);
+    acc = mma(a.y, v[4 * c + 1], acc);
+    acc = mma(a.z, v[4 * c + 2], acc);
+    acc = mma(a.w, v[4 * c + 3], acc);
+#pragma unroll
+    for (int j = 0; j < EPP; ++j) elem(c * EPP + j);
+    __builtin_amdgcn_sched_barrier(0);
+    a = an;
+  }
+}
 
 // Forward: O = sigmoid(Q·Kᵀ·scale + bias [+ score_mod]) · V, one workgroup
 // per (batch, head, 128-query block); keys streamed.
@@ -193,9 +233,10 @@ __global__ __launch_bounds__(64 * FW, fwd_f32_occupancy<D>()) void fwd_f32_kerne
 template <int D, bool CAUSAL, bool SCOREMOD>
 __global__ __launch_bounds__(64 * FW, bwd_f32_occupancy<D>()) void dq_f32_kernel(const KParams p) {
   constexpr int NDB = D / 32;
-  __shared__ __attribute__((aligned(16))) float sK[2][FB * D];
-  __shared__ __attribute__((aligned(16))) float sV[2][FB * D];
-  __shared__ float sC[SCOREMOD ? 2 : 1][FB];
+  constexpr int NS = dq_f32_stages<D>();
+  __shared__ __attribute__((aligned(16))) float sK[NS][FB * D];
+  __shared__ __attribute__((aligned(16))) float sV[NS][FB * D];
+  __shared__ float sC[SCOREMOD ? NS : 1][FB];
 
   const int wg = gap_prologue<4>(p, sK);  // packed layouts: leading gap-zeroing workgroups
   if (wg < 0) return;
@@ -250,33 +291,93 @@ __global__ __launch_bounds__(64 * FW, bwd_f32_occupancy<D>()) void dq_f32_kernel
     dma.issue((uint16_t *)sV[st], (const uint16_t *)Vb, stride_bytes, t * FB, Lk);
   };
 
-  if (ntiles > 0) issue(0, 0);
-  for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    wait_dma();
-    if (SCOREMOD && tid < FB) sC[st][tid] = creg;
-    __syncthreads();
-    if (t + 1 < ntiles) issue(st ^ 1, t + 1);
+  // Element i of a tile (its key 8(i/4) + 4hi + i%4, the lane's query).
+  auto sigma = [&](int st, const f32x16 &s, int i) SIGATTN_INLINE {
+    const float c = SCOREMOD ? sC[st][8 * (i / 4) + 4 * hi + i % 4] : nbl;
+    return sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, c));
+  };
+  auto dsig = [](float pr, float dp) SIGATTN_INLINE {
+    const float u = pr * dp;
+    return __builtin_fmaf(-pr, u, u);  // dP·P·(1 - P)
+  };
+  float ds[16];
+  // Keys at or past seq_lens_k, or (causal) after the lane's query, get
+  // dS = 0 (one branch per tile, after the arithmetic); then dQ += dS·K over
+  // tile t's rows.
+  auto rows = [&](int t) SIGATTN_INLINE {
     const int k0 = t * FB;
-    if (k0 >= wend) continue;
-    f32x16 s = zero16(), dp = zero16();
-    head_product<D>(s, sK[st], qv, l32, hi);
-    head_product<D>(dp, sV[st], ov, l32, hi);
-    const bool mask = k0 + FB > Lk || (CAUSAL && k0 + FB - 1 > qw);
-    float ds[16];
+    if (k0 + FB > Lk || (CAUSAL && k0 + FB - 1 > qw)) {
+      const int lim = (CAUSAL ? min(Lk, myq + 1) : Lk) - k0 - 4 * hi;  // key k0 + 4hi + e valid iff e < lim
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+      for (int i = 0; i < 16; ++i)
+        if (8 * (i / 4) + i % 4 >= lim) ds[i] = 0.0f;
+    }
+    row_product<D>(acc, sK[t % NS], ds, rr);
+  };
+  const int tb = (wend + FB - 1) / FB;  // this wave's key tiles: 0 .. tb-1
+  if constexpr (NS == 2) {
+    if (ntiles > 0) issue(0, 0);
+    for (int t = 0; t < ntiles; ++t) {
+      const int st = t & 1;
+      wait_dma();
+      if (SCOREMOD && tid < FB) sC[st][tid] = creg;
+      // Tile t has landed for every wave, and every wave is done with tile
+      // t-1, whose stage the next copy refills.
+      __syncthreads();
+      if (t + 1 < ntiles) issue(st ^ 1, t + 1);
+      if (t >= tb) continue;
+      f32x16 s = zero16(), dp = zero16();
+      float pr[16];
+      head_product<D>(s, sK[st], qv, l32, hi);
+      head_product_with<D>(dp, sV[st], ov, l32, hi, [&](int i) SIGATTN_INLINE { pr[i] = sigma(st, s, i); });
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 4 * g + r, kr = 8 * g + 4 * hi + r;
-        const float c = SCOREMOD ? sC[st][kr] : nbl;
-        const float pr = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, c));
-        const float u = pr * dp[i];
-        float x = __builtin_fmaf(-pr, u, u);  // dP·P·(1 - P)
-        if (mask && (k0 + kr >= Lk || (CAUSAL && k0 + kr > myq))) x = 0.0f;
-        ds[i] = x;
+      for (int i = 0; i < 16; ++i) ds[i] = dsig(pr[i], dp[i]);
+      rows(t);
+    }
+  } else {
+    // Three stages: iteration t runs tile t+1's S and dP chains with tile t's
+    // arithmetic (inputs from the previous iteration) spread over the dP
+    // chain, then tile t's row products.  Tile t+2 is copied meanwhile into
+    // the stage of tile t-1, which every wave has finished by the barrier of
+    // iteration t.
+    f32x16 s0 = zero16(), p0 = zero16(), s1 = zero16(), p1 = zero16();
+    if (ntiles > 0) {
+      issue(0, 0);
+      wait_dma();
+      if (SCOREMOD && tid < FB) sC[0][tid] = creg;
+      __syncthreads();
+      if (ntiles > 1) issue(1, 1);
+      if (tb > 0) {
+        head_product<D>(s0, sK[0], qv, l32, hi);
+        head_product<D>(p0, sV[0], ov, l32, hi);
       }
-    row_product<D>(acc, sK[st], ds, rr);
+    }
+    auto step = [&](int t, const f32x16 &sc, const f32x16 &pc, f32x16 &sn, f32x16 &pn) SIGATTN_INLINE {
+      if (t + 1 < ntiles) {
+        wait_dma();
+        if (SCOREMOD && tid < FB) sC[(t + 1) % NS][tid] = creg;
+        __syncthreads();
+        if (t + 2 < ntiles) issue((t + 2) % NS, t + 2);
+      }
+      if (t >= tb) return;
+      const int st = t % NS;
+      auto elem = [&](int i) SIGATTN_INLINE { ds[i] = dsig(sigma(st, sc, i), pc[i]); };
+      if (t + 1 < tb) {
+        const int st1 = (t + 1) % NS;
+        sn = zero16();
+        pn = zero16();
+        head_product<D>(sn, sK[st1], qv, l32, hi);
+        head_product_with<D>(pn, sV[st1], ov, l32, hi, elem);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) elem(i);
+      }
+      rows(t);
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+      step(t, s0, p0, s1, p1);
+      if (t + 1 < ntiles) step(t + 1, s1, p1, s0, p0);
+    }
   }
 
   if (myq < p.q_rows_out(Lq)) store_row<D>(dQb + (int64_t)myq * p.sq_t, acc, scale, myq < Lq, hi, half);
@@ -339,31 +440,46 @@ __global__ __launch_bounds__(64 * FW, bwd_f32_occupancy<D>()) void dkdv_f32_kern
     dma.issue((uint16_t *)sO[st], (const uint16_t *)dOm, stride_bytes, t * FB, mend - mstart);
   };
 
+  // This wave's query tiles ta <= t < tb: none for keys past Lk; causal, none
+  // whose queries all precede the wave's first key (tile t ends at query
+  // mstart + 32t + 31).
+  int ta = 0;
+  if (CAUSAL) {
+    const int dd = kw - mstart - FB + 1;
+    ta = dd > 0 ? (dd + FB - 1) / FB : 0;
+  }
+  const int tb = kw >= Lk ? 0 : ntiles;
   if (ntiles > 0) issue(0, 0);
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
     wait_dma();
     __syncthreads();
     if (t + 1 < ntiles) issue(st ^ 1, t + 1);
+    if (t < ta || t >= tb) continue;
     const int m0 = mstart + t * FB;
-    // Nothing to do for keys past Lk, or (causal) queries all before this wave's keys.
-    if (kw >= Lk || (CAUSAL && m0 + FB - 1 < kw)) continue;
     f32x16 s = zero16(), dp = zero16();
-    head_product<D>(s, sQ[st], kv, l32, hi);
-    head_product<D>(dp, sO[st], vv, l32, hi);
-    const bool mask = m0 + FB > Lq || (CAUSAL && m0 < kw + 31);
     float pr[16], ds[16];
+    head_product<D>(s, sQ[st], kv, l32, hi);
+    // P = sigmoid(S) between the dP chain's MFMAs.
+    head_product_with<D>(dp, sO[st], vv, l32, hi, [&](int i) SIGATTN_INLINE {
+      pr[i] = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, nc));
+    });
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int i = 0; i < 16; ++i) {
+      const float u = pr[i] * dp[i];
+      ds[i] = __builtin_fmaf(-pr[i], u, u);
+    }
+    // Queries at or past seq_lens_q, or (causal) before the lane's key: one
+    // branch per tile, after the arithmetic.
+    if (m0 + FB > Lq || (CAUSAL && m0 < kw + 31)) {
+      const int e_end = Lq - m0 - 4 * hi;               // query m0 + 4hi + e valid iff
+      const int e_lo = CAUSAL ? myk - m0 - 4 * hi : 0;  // e_lo <= e < e_end
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 4 * g + r, q = m0 + 8 * g + 4 * hi + r;
-        float x = sigmoid_from_neg_log2(__builtin_fmaf(s[i], nsl, nc));
-        if (mask && (q >= Lq || (CAUSAL && myk > q))) x = 0.0f;
-        const float u = x * dp[i];
-        pr[i] = x;
-        ds[i] = __builtin_fmaf(-x, u, u);
+      for (int i = 0; i < 16; ++i) {
+        const int e = 8 * (i / 4) + i % 4;
+        if (e >= e_end || e < e_lo) pr[i] = ds[i] = 0.0f;
       }
+    }
     row_product<D>(dva, sO[st], pr, rr);
     row_product<D>(dka, sQ[st], ds, rr);
   }
