@@ -229,15 +229,16 @@ def kernel_times(cfg, q, k, v, do, iters: int, seq_lens=None, packed=False):
         # at D <= 64 the library runs both kernels as one launch.
         calls["bwd"] = lambda: lib.sigattn_bwd_split(ctypes.byref(pr), do.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                                                      dv.data_ptr(), sptr, sbytes, stream)
-    # Median of three timed runs of `iters` launches each: the first kernel
-    # timed after a long step loop can read 10-20 % slow on its own.
+    # Median of five timed runs of `iters` launches each: the first kernel
+    # timed after a long step loop, or early in a process, can read 5-20 %
+    # slow on its own.
     out = {}
     for name, fn in calls.items():
         for _ in range(3):
             assert fn() == 0
         torch.cuda.synchronize()
         runs = []
-        for _ in range(3):
+        for _ in range(5):
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
             for _ in range(iters):
@@ -822,33 +823,43 @@ def measure_config(name: str, steps: int, warmup: int) -> dict:
 def padded_block(cfg, q, k, v, do, sl, kt, P, iters) -> dict:
     """The padded path's TFLOPS per valid token as a fraction of dense: the
     dense kernels at the full shape and the padded kernels, timed in the same
-    run through the C ABI (kernel sums fwd + dQ + dK/dV), plus the packed
-    layout (the same sequences as [rows, H, D] with cu_seqlens)."""
+    run through the C ABI, plus the packed layout (the same sequences as
+    [rows, H, D] with cu_seqlens).  padded_vs_dense times the forward and the
+    whole backward as the library launches them for the public API (for large
+    ragged non-causal problems its two kernels run concurrently);
+    kernel_sum_padded_vs_dense the three kernels launched one at a time."""
     B, L, H, D, causal = cfg["B"], cfg["L"], cfg["H"], cfg["D"], cfg["causal"]
     kd = kernel_times(cfg, q, k, v, do, iters=iters)
     Pd = pairs(L, causal) * B * H
-    # Per-kernel sums (the padded problems never take the one-launch backward).
-    dense_tf = 14 * D * Pd / (sum(kd[n] for n in KERNELS) * 1e-3) / 1e12
-    padded_tf = 14 * D * P / (sum(kt[n] for n in KERNELS) * 1e-3) / 1e12
     kp = kernel_times(cfg, q, k, v, do, iters=iters, seq_lens=sl, packed=True)
-    packed_tf = 14 * D * P / (sum(kp[n] for n in KERNELS) * 1e-3) / 1e12
     log("[bench] packed layout kernels (ms): " + ", ".join(f"{n}={t:.3f}" for n, t in kp.items()))
+
+    def tflops(pairs_, kt_, parts):
+        return 14 * D * pairs_ / (sum(kt_[n] for n in parts) * 1e-3) / 1e12
+
+    launched, kernels = ("fwd", "bwd"), KERNELS
+    dense_tf, padded_tf, packed_tf = tflops(Pd, kd, launched), tflops(P, kt, launched), tflops(P, kp, launched)
+    dense_ks, padded_ks, packed_ks = tflops(Pd, kd, kernels), tflops(P, kt, kernels), tflops(P, kp, kernels)
     credit = {"fwd": 4 * D * P, "bwd_dq": 2 * D * P, "bwd_dkdv": 8 * D * P}
     credit_d = {"fwd": 4 * D * Pd, "bwd_dq": 2 * D * Pd, "bwd_dkdv": 8 * D * Pd}
     info = {
         "seq_lens": sl.tolist(),
         "valid_pair_fraction": round(P / Pd, 4),
         "padded_vs_dense": round(padded_tf / dense_tf, 4),
+        "packed_vs_dense": round(packed_tf / dense_tf, 4),
+        "kernel_sum_padded_vs_dense": round(padded_ks / dense_ks, 4),
+        "kernel_sum_packed_vs_dense": round(packed_ks / dense_ks, 4),
         "per_kernel_padded_vs_dense": {
             n: round((credit[n] / kt[n]) / (credit_d[n] / kd[n]), 4) for n in ("fwd", "bwd_dq", "bwd_dkdv")},
         "padded_kernel_ms": {n: round(t, 4) for n, t in kt.items()},
         "dense_kernel_ms": {n: round(t, 4) for n, t in kd.items()},
+        "packed_kernel_ms": {n: round(t, 4) for n, t in kp.items()},
         "padded_kernel_tflops": round(padded_tf, 2),
         "padded_kernel_pct_of_peak": round(100 * padded_tf / PEAK_BF16_TFLOPS, 2),
         "dense_kernel_tflops": round(dense_tf, 2),
         "packed_kernel_tflops": round(packed_tf, 2),
-        "packed_vs_dense": round(packed_tf / dense_tf, 4),
-        "note": "kernel sums (fwd + dQ + dK/dV) through the C ABI; padded and packed (the same "
+        "note": "padded_vs_dense: fwd + the whole backward as the library launches it, through the C ABI; "
+                "kernel_sum_*: fwd + dQ + dK/dV launched one at a time; padded and packed (the same "
                 "sequences as [rows, H, D] with cu_seqlens) count valid pairs only",
     }
     log(f"[bench] padded {info}")

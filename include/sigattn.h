@@ -168,7 +168,14 @@ int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream);
  * rows get dq = 0, padded key rows get dk = dv = 0.  Dense f16/bf16 problems
  * at head_dim <= 64 whose dQ and dK/dV grids (128 rows per workgroup)
  * together fit one workgroup per compute unit run both kernels' work as one
- * launch, bit-identical to the two launches.
+ * launch, bit-identical to the two launches.  Ragged (seq_lens or cu_seqlens)
+ * non-causal f16/bf16 problems at head_dim 64 with at least eight 128-query
+ * blocks per compute unit run the two kernels concurrently: the dK/dV kernel
+ * on a second stream the library keeps per device (default priority),
+ * forked off `stream` by an event and joined back by another, so the call
+ * stays ordered on `stream` like any other; the events are the calling host
+ * thread's own.  Under stream capture both kernels stay on `stream`.
+ * Results equal the sequential launches' bit for bit.
  */
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,
                 void *dv, void *stream);

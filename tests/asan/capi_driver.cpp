@@ -17,6 +17,7 @@ std::vector<std::string> g_calls;
 std::vector<sigattn::KParams> g_hist;  // parameters of each launch since the last calls()
 sigattn::KParams g_last{};
 int g_D = 0;  // head dim passed to the last kernel launch
+hipStream_t g_dq_stream = nullptr, g_dkdv_stream = nullptr;  // streams of the last dQ / dK/dV launches
 int g_fail = 0;
 
 void record(const char *name, const sigattn::KParams &p) {
@@ -78,12 +79,14 @@ void launch_fwd_mfma(const KParams &p, int, int D, bool, bool, hipStream_t) {
   g_D = D;
   record("fwd_mfma", p);
 }
-void launch_bwd_dq_mfma(const KParams &p, int, int D, bool, bool, hipStream_t) {
+void launch_bwd_dq_mfma(const KParams &p, int, int D, bool, bool, hipStream_t st) {
   g_D = D;
+  g_dq_stream = st;
   record("dq_mfma", p);
 }
-void launch_bwd_dkdv_mfma(const KParams &p, int, int D, bool, bool, bool dsout, hipStream_t) {
+void launch_bwd_dkdv_mfma(const KParams &p, int, int D, bool, bool, bool dsout, hipStream_t st) {
   g_D = D;
+  g_dkdv_stream = st;
   record(dsout ? "dkdv_mfma_ds" : "dkdv_mfma", p);
 }
 void launch_bwd_dq_ds_mfma(const KParams &p, int, int, bool, hipStream_t) { record("dq_ds", p); }
@@ -150,6 +153,41 @@ extern "C" hipError_t hipGetDevice(int *dev) {
 extern "C" hipError_t hipDeviceGetAttribute(int *value, hipDeviceAttribute_t, int) {
   *value = g_cus;
   return hipSuccess;
+}
+// The concurrent backward's second stream and its fork / join events: fake
+// handles, every record and wait logged as "record <event> <stream>" /
+// "wait <stream> <event>" (handles as small numbers; stream 0 = the caller's
+// null stream), and a capture status the checks set.
+static hipStreamCaptureStatus g_capture = hipStreamCaptureStatusNone;
+static int g_nevents = 0;
+static std::vector<std::string> g_sync;
+static const hipStream_t kSide = (hipStream_t)(uintptr_t)0x5100;
+static std::string handle(const void *h) { return std::to_string((unsigned long)(uintptr_t)h); }
+extern "C" hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus *status) {
+  *status = g_capture;
+  return hipSuccess;
+}
+extern "C" hipError_t hipStreamCreateWithFlags(hipStream_t *stream, unsigned int) {
+  *stream = kSide;
+  return hipSuccess;
+}
+extern "C" hipError_t hipEventCreateWithFlags(hipEvent_t *event, unsigned) {
+  *event = (hipEvent_t)(uintptr_t)(0x100 + ++g_nevents);
+  return hipSuccess;
+}
+extern "C" hipError_t hipEventRecord(hipEvent_t event, hipStream_t stream) {
+  g_sync.push_back("record " + handle(event) + " " + handle(stream));
+  return hipSuccess;
+}
+extern "C" hipError_t hipStreamWaitEvent(hipStream_t stream, hipEvent_t event, unsigned int) {
+  g_sync.push_back("wait " + handle(stream) + " " + handle(event));
+  return hipSuccess;
+}
+static std::string sync_log() {
+  std::string s;
+  for (auto &c : g_sync) s += (s.empty() ? "" : ";") + c;
+  g_sync.clear();
+  return s;
 }
 
 // The fp32 kernels' LDS tiles (32 rows x D floats, four waves copying): the
@@ -522,6 +560,51 @@ int main() {
     c = base(2, 1024, 8, 64);
     c.dtype = SIGATTN_F32;
     EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, nullptr) == 0 && calls() == "dq_f32,dkdv_f32");
+    EXPECT(g_sync.empty());
+    // The concurrent recompute backward: ragged, non-causal, D = 64, at least
+    // eight 128-query blocks per CU (B=4 T=8192 H=12: 3072 on 256 CUs).  The
+    // dK/dV kernel goes first, on the side stream, forked off the caller's
+    // stream (0 here) by event 257 and joined back by event 258.
+    c = base(4, 8192, 12, 64);
+    c.seq_lens_q = c.seq_lens_k = (const int32_t *)kFake;
+    const hipStream_t own = nullptr;
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dkdv_mfma,dq_mfma" &&
+           g_dkdv_stream == kSide && g_dq_stream == own);
+    EXPECT(sync_log() == "record 257 0;wait 20736 257;record 258 20736;wait 0 258");
+    // Again on this thread: the same stream and events.
+    EXPECT(sigattn_bwd_split(&c, kFake, kFake, kFake, kFake, nullptr, 0, own) == 0 &&
+           calls() == "dkdv_mfma,dq_mfma" && g_dkdv_stream == kSide && g_nevents == 2);
+    EXPECT(sync_log() == "record 257 0;wait 20736 257;record 258 20736;wait 0 258");
+    // The packed layout alike; the dQ launch zeroes the gap rows (none here).
+    sigattn_problem pk = c;
+    pk.seq_lens_q = pk.seq_lens_k = nullptr;
+    pk.cu_seqlens_q = pk.cu_seqlens_k = (const int32_t *)kFake;
+    pk.rows_q = pk.rows_k = 4 * 8192;
+    pk.q_stride_b = pk.k_stride_b = 0;
+    EXPECT(sigattn_bwd(&pk, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dkdv_mfma,dq_mfma" &&
+           g_dkdv_stream == kSide);
+    EXPECT(!sync_log().empty());
+    // Under stream capture, causal, dense, D = 128 or too few blocks: one stream.
+    g_capture = hipStreamCaptureStatusActive;
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma" &&
+           g_dkdv_stream == own);
+    g_capture = hipStreamCaptureStatusNone;
+    sigattn_problem d = c;
+    d.causal = 1;
+    EXPECT(sigattn_bwd(&d, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    d = c;
+    d.seq_lens_q = d.seq_lens_k = nullptr;
+    EXPECT(sigattn_bwd(&d, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    d = base(4, 8192, 12, 32);
+    d.seq_lens_q = d.seq_lens_k = (const int32_t *)kFake;
+    EXPECT(sigattn_bwd(&d, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    d = base(4, 4096, 8, 64);  // 1024 blocks: four per CU
+    d.seq_lens_q = d.seq_lens_k = (const int32_t *)kFake;
+    EXPECT(sigattn_bwd(&d, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma");
+    // Halves alone run on the caller's stream.
+    EXPECT(sigattn_bwd_dq(&c, kFake, kFake, own) == 0 && calls() == "dq_mfma" && g_dq_stream == own);
+    EXPECT(sigattn_bwd_dkdv(&c, kFake, kFake, kFake, own) == 0 && calls() == "dkdv_mfma" && g_dkdv_stream == own);
+    EXPECT(g_sync.empty());
     g_cus = 0;
   }
   if (g_fail == 0) std::printf("capi sanitizer driver: all checks passed\n");

@@ -44,6 +44,14 @@ def _case(kind):
         cu = torch.tensor([0, 210, 210, 571], dtype=torch.int32, device=DEV)
         return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention_varlen(q, k, v, cu, cu, 300, 300,
                                                                            is_causal=True)
+    if kind == "padded_d64_concurrent_bwd":
+        # Large enough (B·H·T/128 = 2048 query blocks, eight per CU) for the
+        # eager backward to run its two kernels on two streams; under capture
+        # the library keeps them on the capturing stream.
+        B, T, H, D, dtype = 2, 4096, 32, 64, torch.float16
+        q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
+        sl = torch.tensor([4096, 2500], dtype=torch.int32, device=DEV)
+        return (q, k, v, do), lambda q, k, v: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl)
     B, T, H, D, dtype = 3, 200, 2, 64, torch.float16
     q, k, v, do = (randn((B, T, H, D), dtype, DEV, g) for _ in range(4))
     sl = torch.tensor([200, 77, 130], dtype=torch.int32, device=DEV)
@@ -51,7 +59,8 @@ def _case(kind):
 
 
 @pytest.mark.parametrize("kind", ["dense_d128_causal", "dense_d64_range_split", "padded_d64",
-                                  "dense_d64_one_launch_bwd", "fp32_d128", "packed_d64_gaps"])
+                                  "dense_d64_one_launch_bwd", "fp32_d128", "packed_d64_gaps",
+                                  "padded_d64_concurrent_bwd"])
 def test_graph_replays_match_eager(kind):
     (q, k, v, do), attn = _case(kind)
     leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]

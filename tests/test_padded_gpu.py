@@ -2,6 +2,7 @@
 myops::sigmoid_attn_padded_fwd/bwd -> libsigattn.so).  Mirrors the reference's
 tests/test_sigmoid_padded.py."""
 
+import ctypes
 import math
 
 import numpy as np
@@ -9,6 +10,7 @@ import pytest
 import torch
 
 import triton_sigmoid as ts
+from triton_sigmoid import _capi
 from conftest import get_tolerance
 from helpers import (assert_close_to_oracle, assert_reference_criterion, criterion_errors,
                      oracle_fwd_bwd, randn, to_np)
@@ -304,3 +306,38 @@ def test_head_major_layout_equals_contiguous(D, causal):
         assert torch.equal(got, ref), f"{name} differs from the contiguous layout"
         for b in range(B):
             assert torch.all(got[b, int(lens[b]):] == 0), f"{name}: padding rows of batch {b} not zero"
+
+
+@pytest.mark.parametrize("layout", ["padded", "packed"])
+def test_concurrent_backward_equals_the_two_kernels(layout):
+    """A ragged non-causal D = 64 problem of 2048 query blocks (eight per CU of
+    the MI355X) runs its recompute backward's dQ and dK/dV kernels on two
+    streams; its dQ, dK and dV equal those of the two kernels run alone, one
+    after the other on one stream (sigattn_bwd_dq, sigattn_bwd_dkdv), bit for
+    bit, with the padding rows zero."""
+    B, T, H, D, dtype = 2, 4096, 32, 64, torch.float16
+    q, k, v, do, sq, sk = _case(B, T, T, H, D, dtype, seed=91, noise=False)
+    sq = sk = torch.tensor([4096, 2731], dtype=torch.int32)
+    lib = _capi.load_library()
+    bias = -torch.log(sk.float()).to(DEV)
+    scale = torch.full((), 1 / math.sqrt(D), dtype=torch.float32, device=DEV)
+    if layout == "packed":
+        lens = sq.tolist()
+        q, k, v, do = (torch.cat([t[b, :n] for b, n in enumerate(lens)], 0).contiguous() for t in (q, k, v, do))
+        cu = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32, device=DEV)
+        pr = _capi._problem(q, k, v, bias, None, scale, None, None, False, packed=(cu, cu, T, T))
+    else:
+        pr = _capi._problem(q, k, v, bias, None, scale, sq.to(DEV), sk.to(DEV), False)
+    stream = torch.cuda.current_stream().cuda_stream
+    one = [torch.full_like(t, float("nan")) for t in (q, k, v)]
+    two = [torch.full_like(t, float("nan")) for t in (q, k, v)]
+    assert lib.sigattn_bwd(ctypes.byref(pr), do.data_ptr(), *(t.data_ptr() for t in one), stream) == 0
+    assert lib.sigattn_bwd_dq(ctypes.byref(pr), do.data_ptr(), two[0].data_ptr(), stream) == 0
+    assert lib.sigattn_bwd_dkdv(ctypes.byref(pr), do.data_ptr(), two[1].data_ptr(), two[2].data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), one, two):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), name
+    if layout == "padded":
+        for t in one:
+            assert torch.all(t[1, 2731:] == 0)

@@ -1,15 +1,18 @@
 // C ABI of libsigattn.so (declared in include/sigattn.h).
 //
 // Validation runs on the host before any HIP call, so every error path is
-// testable without a GPU.  Dispatch: f16/bf16 with D in {64, 128} and 16-byte
-// aligned rows take the MFMA kernels; everything else takes the portable
-// kernels.  Launches are asynchronous on the caller's stream; nothing here
-// allocates or synchronises.
+// testable without a GPU.  Dispatch: rows starting on 16-byte boundaries take
+// the MFMA kernels (f16/bf16 the 16-bit ones, fp32 the fp32 ones; D in {16,
+// 32, 64, 128}); everything else takes the portable kernels.  Launches are
+// asynchronous and ordered on the caller's stream (the concurrent recompute
+// backward forks a second stream off it and joins it back); nothing here
+// allocates device memory or synchronises the host.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
 #include <climits>
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/sigattn.h"
 #include "launch.h"
@@ -142,6 +145,86 @@ bool fuse_backward(const sigattn_problem *p) {
   const int64_t wgs = p->B * p->H * (cdiv(p->Tq, 128) + cdiv(p->Tk, 128));
   return cus > 0 && wgs <= cus;
 }
+
+// The recompute backward's dQ and dK/dV kernels run concurrently, dK/dV on a
+// second stream, for ragged non-causal problems at head_dim 64 with at least
+// eight 128-query blocks per CU: the items of such a grid have the lengths of
+// their sequences, so each kernel ends in a drain of unevenly finishing
+// workgroups, which the other kernel's workgroups fill.  Measured at B=4
+// Lmax=8192 H=12 (seq_lens 1078-5599): 603 -> 577 us.  Dense problems of the
+// same shape gain nothing (2876 -> 2879 us), and at B=8 Lmax=2048 H=8 causal,
+// padded or dense, both kernels on one stream are faster (103-112 against
+// 114-121 us padded), so those stay sequential.
+#ifndef SIGATTN_CONCURRENT_BWD
+#define SIGATTN_CONCURRENT_BWD 1
+#endif
+bool concurrent_backward(const sigattn_problem *p) {
+  if (!SIGATTN_CONCURRENT_BWD || !is_ragged(p) || p->causal != 0 || mfma_head_dim(p) != 64) return false;
+  const int64_t cus = sigattn::device_compute_units();
+  return cus > 0 && p->B * p->H * cdiv(p->Tq, 128) >= 8 * cus;
+}
+
+// Fork / join of a second stream around the caller's: fork() makes the
+// device's side stream (created on first use, default priority, never
+// destroyed) wait for the work queued on `st` so far and returns it; join()
+// makes `st` wait for the work then queued on the side stream.  The events
+// are this host thread's own (a fork records into them and the next fork of
+// the same thread may reuse them once its waits are queued), so host threads
+// never race on them; threads sharing the side stream only order their
+// side-stream work one after the other.  Returns nullptr -- run everything on
+// `st` -- under stream capture or when a runtime call fails.
+class SideStream {
+ public:
+  hipStream_t fork(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    int dev = -1;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+        hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    hipStream_t side = stream(dev);
+    Events &ev = events_[dev];
+    if (side == nullptr || !ev.ready() || hipEventRecord(ev.fork, st) != hipSuccess ||
+        hipStreamWaitEvent(side, ev.fork, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    dev_ = dev;
+    return side;
+  }
+  // Returns false if the join could not be queued (then the caller's stream
+  // is not ordered after the side stream's work: an error to report).
+  bool join(hipStream_t st, hipStream_t side) {
+    Events &ev = events_[dev_];
+    return hipEventRecord(ev.join, side) == hipSuccess && hipStreamWaitEvent(st, ev.join, 0) == hipSuccess;
+  }
+
+ private:
+  static constexpr int kMaxDevices = 64;
+  struct Events {
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool ready() {
+      if (fork == nullptr && hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess) fork = nullptr;
+      if (join == nullptr && hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) join = nullptr;
+      return fork != nullptr && join != nullptr;
+    }
+  };
+  static hipStream_t stream(int dev) {
+    static std::mutex mu;
+    static hipStream_t streams[kMaxDevices];
+    std::lock_guard<std::mutex> lock(mu);
+    if (streams[dev] == nullptr) {
+      hipStream_t s = nullptr;
+      if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+      streams[dev] = s;
+    }
+    return streams[dev];
+  }
+  Events events_[kMaxDevices];
+  int dev_ = 0;
+};
+thread_local SideStream t_side;
 
 // Fewest rows of the streamed range (keys for the forward and dQ kernels,
 // queries for dK/dV) that a range-split chunk takes; chunks of at least twice
@@ -572,14 +655,21 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
     }
     return launch_status();
   }
-  // Recompute backward.  Both kernels go on the caller's stream, one after
-  // the other: each fills the GPU on its own and they cannot share a CU
-  // (their LDS footprints add up to more than one CU holds), so running them
-  // concurrently on two streams only made both slower (measured).
+  // Recompute backward.  The two kernels are independent (the sigmoid's
+  // backward needs no forward statistics): one launch on small dense grids
+  // (fuse_backward), concurrently on two streams for large ragged non-causal
+  // ones (concurrent_backward), else one after the other on the caller's
+  // stream -- each then fills the GPU on its own, and concurrent launches
+  // measured slower there.
   if (need_dq && need_dkdv && mfma && fuse_backward(p)) {
     sigattn::launch_bwd_fused_mfma(k, dt, D, causal, sm, st);
     return launch_status();
   }
+  // Concurrent: the dK/dV kernel (the longer one) is queued first, on the
+  // side stream, then the dQ kernel on the caller's.
+  hipStream_t side = nullptr;
+  if (need_dq && need_dkdv && mfma && concurrent_backward(p)) side = t_side.fork(st);
+  if (side != nullptr) sigattn::launch_bwd_dkdv_mfma(k, dt, D, causal, sm, false, side);
   KParams kq = k;
   if (dq_gaps) use_gaps(kq, gq, gk);
   if (need_dq) {
@@ -587,11 +677,12 @@ static int bwd_impl(const sigattn_problem *p, const void *dout, void *dq, void *
     else if (f32mma) sigattn::launch_bwd_dq_f32(kq, D, causal, sm, st);
     else sigattn::launch_bwd_dq_generic(k, dt, D, causal, st);
   }
-  if (need_dkdv) {
+  if (need_dkdv && side == nullptr) {
     if (mfma) sigattn::launch_bwd_dkdv_mfma(k, dt, D, causal, sm, false, st);
     else if (f32mma) sigattn::launch_bwd_dkdv_f32(k, D, causal, sm, st);
     else sigattn::launch_bwd_dkdv_generic(k, dt, D, causal, st);
   }
+  if (side != nullptr && !t_side.join(st, side)) return SIGATTN_ERR_LAUNCH;
   return launch_status();
 }
 
