@@ -47,6 +47,32 @@ def test_dense_matches_oracle(dtype, D, T, causal):
     assert_close_to_oracle(v.grad, dv, dtype, "dV")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [33, 64, 65, 96])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_mod", [False, True])
+def test_fp32_few_key_tiles_match_oracle(D, T, causal, with_mod):
+    """fp32 lengths of two and three 32-row tiles: the D = 128 dQ kernel
+    runs tile t's sigmoid arithmetic under tile t+1's MFMA chains over a
+    three-stage ring, whose first and last iterations (and, causal, each
+    wave's own last tile) these cover; score_mod sits in that ring too."""
+    B, H = 2, 3
+    dtype = torch.float32
+    q, k, v, do = _inputs(B, T, H, D, dtype, seed=T * 5 + D + causal)
+    sm = torch.randn((B, T), generator=torch.Generator().manual_seed(T)).to(DEV) if with_mod else None
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention(q, k, v, is_causal=causal, score_mod=sm)
+    o.backward(do)
+    bias = np.full(B, -math.log(T), dtype=np.float32).astype(np.float64)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(q, k, v, do, scale=np.float32(1.0 / math.sqrt(D)), bias=bias,
+                                          score_mod=sm, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+
+
 @pytest.mark.parametrize("H", [1, 5, 12])
 @pytest.mark.parametrize("D", [16, 32, 64, 128])
 def test_various_num_heads_match_oracle(H, D):
