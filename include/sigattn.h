@@ -174,7 +174,8 @@ int sigattn_fwd_noalloc(const sigattn_problem *p, void *out, void *stream);
  * on a second stream the library keeps per device (default priority),
  * forked off `stream` by an event and joined back by another, so the call
  * stays ordered on `stream` like any other; the events are the calling host
- * thread's own.  Under stream capture both kernels stay on `stream`.
+ * thread's own.  Under stream capture, or on a stream of another device than
+ * the current one, both kernels stay on `stream`.
  * Results equal the sequential launches' bit for bit.
  */
 int sigattn_bwd(const sigattn_problem *p, const void *dout, void *dq, void *dk,

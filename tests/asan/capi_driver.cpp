@@ -167,6 +167,12 @@ extern "C" hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus *
   *status = g_capture;
   return hipSuccess;
 }
+// Streams belong to device 0, except kOtherDevice.
+static const hipStream_t kOtherDevice = (hipStream_t)(uintptr_t)0x7700;
+extern "C" hipError_t hipStreamGetDevice(hipStream_t stream, hipDevice_t *device) {
+  *device = stream == kOtherDevice ? 1 : 0;
+  return hipSuccess;
+}
 extern "C" hipError_t hipStreamCreateWithFlags(hipStream_t *stream, unsigned int) {
   *stream = kSide;
   return hipSuccess;
@@ -584,7 +590,10 @@ int main() {
     EXPECT(sigattn_bwd(&pk, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dkdv_mfma,dq_mfma" &&
            g_dkdv_stream == kSide);
     EXPECT(!sync_log().empty());
-    // Under stream capture, causal, dense, D = 128 or too few blocks: one stream.
+    // On another device's stream, under stream capture, causal, dense, D = 32
+    // or too few blocks: one stream.
+    EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, kOtherDevice) == 0 && calls() == "dq_mfma,dkdv_mfma" &&
+           g_dkdv_stream == kOtherDevice && g_dq_stream == kOtherDevice && g_sync.empty());
     g_capture = hipStreamCaptureStatusActive;
     EXPECT(sigattn_bwd(&c, kFake, kFake, kFake, kFake, own) == 0 && calls() == "dq_mfma,dkdv_mfma" &&
            g_dkdv_stream == own);

@@ -172,14 +172,18 @@ bool concurrent_backward(const sigattn_problem *p) {
 // the same thread may reuse them once its waits are queued), so host threads
 // never race on them; threads sharing the side stream only order their
 // side-stream work one after the other.  Returns nullptr -- run everything on
-// `st` -- under stream capture or when a runtime call fails.
+// `st` -- under stream capture, when `st` belongs to another device than the
+// current one (the side stream is the current device's), or when a runtime
+// call fails.
 class SideStream {
  public:
   hipStream_t fork(hipStream_t st) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     int dev = -1;
+    hipDevice_t sdev = -1;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
-        hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices ||
+        hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) {
       (void)hipGetLastError();
       return nullptr;
     }
