@@ -206,6 +206,71 @@ def test_padded_reference_criterion(dtype, B, H, Tq, Tk, D, causal):
     assert_reference_criterion(errs, tol)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("Tq,Tk", [(128, 128), (200, 77), (77, 300)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_score_mod_matches_oracle(dtype, D, Tq, Tk, causal):
+    """score_mod [B, Tk] on the padded path, forward and backward against the
+    float64 oracle at every head dim and dtype (the reference checks one fp16
+    D = 64 case, tests/test_sigmoid_padded.py:387-477).  The score_mod entries
+    of padding keys hold NaN: like the padding rows of Q/K/V they must never
+    be read."""
+    B, H = 3, 2
+    q, k, v, do, sq, sk = _case(B, Tq, Tk, H, D, dtype, seed=7 * Tq + Tk + D + int(causal))
+    g = torch.Generator().manual_seed(Tq + 5 * D)
+    sm = (torch.randn((B, Tk), generator=g) * 2.0).to(dtype).to(DEV)
+    sm_noisy = sm.clone()
+    for b in range(B):
+        sm_noisy[b, int(sk[b]):] = float("nan")
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, seq_lens_q=sq, is_causal=causal, score_mod=sm_noisy)
+    o.backward(do)
+    bias = (-torch.log(sk.float())).double().cpu().numpy()
+    qc, kc, vc, doc = _clean(q, sq), _clean(k, sk), _clean(v, sk), _clean(do, sq)
+    want_o, (dq, dk, dv) = oracle_fwd_bwd(qc, kc, vc, doc, scale=np.float32(1 / math.sqrt(D)), bias=bias,
+                                          score_mod=_clean(sm, sk), seq_lens_q=sq, seq_lens_k=sk, causal=causal)
+    assert_close_to_oracle(o, want_o, dtype, "O")
+    assert_close_to_oracle(q.grad, dq, dtype, "dQ")
+    assert_close_to_oracle(k.grad, dk, dtype, "dK")
+    assert_close_to_oracle(v.grad, dv, dtype, "dV")
+    for b in range(B):
+        assert torch.all(o[b, sq[b]:] == 0) and torch.all(q.grad[b, sq[b]:] == 0)
+        assert torch.all(k.grad[b, sk[b]:] == 0) and torch.all(v.grad[b, sk[b]:] == 0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_padded_score_mod_reference_criterion(dtype):
+    """The reference's test_score_mod_padded (tests/test_sigmoid_padded.py:387-477):
+    B=2 L=128 H=4 D=64, N(0, 0.5²) inputs, score_mod ~ N(0, 1) in the input
+    dtype, seq_lens_k = [100, 110] and no seq_lens_q; errors against the fp32
+    eager path within 2x (forward) / 3x (backward) the mixed-precision eager
+    path's plus the tolerance, the gradients of padding keys excluded.  Its
+    absolute bounds (O, dQ and dK below the tolerance, dV below twice it) are
+    checked in fp16, the dtype the reference runs this test in: one bf16
+    rounding step of the dV entries in [2, 4) this case produces is 2^-6,
+    above twice the bf16 tolerance, for any kernel that stores bf16."""
+    B, L, H, D = 2, 128, 4, 64
+    tol = get_tolerance(dtype)
+    g = torch.Generator().manual_seed(387)
+    q, k, v = (randn((B, L, H, D), dtype, DEV, g, 0.5) for _ in range(3))
+    do = randn((B, L, H, D), dtype, DEV, g)
+    sm = randn((B, L), dtype, DEV, g)
+    sk = torch.tensor([100, 110], dtype=torch.int32, device=DEV)
+    k_valid = torch.arange(L)[None, :] < sk.cpu()[:, None]
+    errs = criterion_errors(
+        q, k, v, do,
+        lambda a, b, c: ts.sigmoid_attention_padded(a, b, c, seq_lens_k=sk, score_mod=sm),
+        dict(seq_lens_k=sk, score_mod=sm), k_valid=k_valid)
+    for name, (e, em) in errs.items():
+        assert e <= (2.0 if name == "O" else 3.0) * em + tol, (name, e, em, tol)
+        if dtype == torch.float16:
+            assert e < (2.0 * tol if name == "dV" else tol), (name, e, tol)
+    out_none = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sk, score_mod=None)
+    assert out_none.shape == (B, L, H, D)
+
+
 def test_padding_noise_invariance():
     B, T, H, D = 2, 300, 2, 64
     q, k, v, do, sq, sk = _case(B, T, T, H, D, torch.bfloat16, seed=3, noise=False)
