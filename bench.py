@@ -481,43 +481,49 @@ def sweep():
     benchmarks/benchmark_sigmoid.py:91-93); fwd and backward-only
     (o.backward(dO, retain_graph=True)), timed by bench_like_reference.
     The H100 chart has no 50 % panel, so those rows carry no comparison."""
+    return [sweep_row(hd, pad, L) for hd in (64, 128) for pad in (0, 25, 50) for L in SWEEP_L]
+
+
+def sweep_row(hd: int, pad: int, L: int) -> dict:
+    """One point of the reference benchmark's grid (see sweep)."""
     import torch
     import triton_sigmoid as ts
     dev = torch.device("cuda", 0)
-    rows = []
-    for hd in (64, 128):
-        for pad in (0, 25, 50):
-            for li, L in enumerate(SWEEP_L):
-                B, H = 16384 // L, 2048 // hd
-                g = torch.Generator().manual_seed(L * 1000 + hd * 10 + pad)
-                q, k, v = (torch.randn((B, L, H, hd), generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
-                           for _ in range(3))
-                if pad:
-                    lo = max(1, int(L * (1 - pad / 100)))
-                    sl = torch.randint(lo, L + 1, (B,), generator=g, dtype=torch.int32).to(dev)
-                    attn = lambda: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl,
-                                                               is_causal=False, sigmoid_bias=0.0)
-                    flops_fwd = 4 * H * hd * float((sl.double() ** 2).sum().item())
-                else:
-                    attn = lambda: ts.sigmoid_attention(q, k, v, sigmoid_bias=0.0)
-                    flops_fwd = 4.0 * B * H * L * L * hd
-                ms_f = bench_like_reference(attn, grad_to_none=(q, k, v))
-                o = attn()
-                do = torch.randn(o.shape, generator=g).to(torch.bfloat16).to(dev)
-                ms_b = bench_like_reference(lambda: o.backward(do, retain_graph=True), grad_to_none=(q, k, v))
-                h100 = {m: H100_CHART[(m, hd, pad)][li] if (m, hd, pad) in H100_CHART else None
-                        for m in ("fwd", "bwd")}
-                row = {"D": hd, "L": L, "B": B, "H": H, "padding_pct": pad,
-                       "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
-                       "fwd_tflops": round(flops_fwd / ms_f / 1e9, 1),
-                       "bwd_tflops": round(2.5 * flops_fwd / ms_b / 1e9, 1),
-                       "h100_fwd": h100["fwd"], "h100_bwd": h100["bwd"]}
-                rows.append(row)
-                log(f"[sweep] D={hd} L={L} B={B} H={H} pad={pad}%: fwd {row['fwd_tflops']} TFLOPS "
-                    f"(H100 {row['h100_fwd']}), bwd {row['bwd_tflops']} (H100 {row['h100_bwd']})")
-                del q, k, v, o, do
-                torch.cuda.empty_cache()
-    return rows
+    li = SWEEP_L.index(L)
+    B, H = 16384 // L, 2048 // hd
+    g = torch.Generator().manual_seed(L * 1000 + hd * 10 + pad)
+    q, k, v = (torch.randn((B, L, H, hd), generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+               for _ in range(3))
+    if pad:
+        lo = max(1, int(L * (1 - pad / 100)))
+        sl = torch.randint(lo, L + 1, (B,), generator=g, dtype=torch.int32).to(dev)
+        attn = lambda: ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl,  # noqa: E731
+                                                   is_causal=False, sigmoid_bias=0.0)
+        flops_fwd = 4 * H * hd * float((sl.double() ** 2).sum().item())
+    else:
+        attn = lambda: ts.sigmoid_attention(q, k, v, sigmoid_bias=0.0)  # noqa: E731
+        flops_fwd = 4.0 * B * H * L * L * hd
+    ms_f = bench_like_reference(attn, grad_to_none=(q, k, v))
+    o = attn()
+    do = torch.randn(o.shape, generator=g).to(torch.bfloat16).to(dev)
+    ms_b = bench_like_reference(lambda: o.backward(do, retain_graph=True), grad_to_none=(q, k, v))
+    h100 = {m: H100_CHART[(m, hd, pad)][li] if (m, hd, pad) in H100_CHART else None for m in ("fwd", "bwd")}
+    row = {"D": hd, "L": L, "B": B, "H": H, "padding_pct": pad,
+           "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
+           "fwd_tflops": round(flops_fwd / ms_f / 1e9, 1),
+           "bwd_tflops": round(2.5 * flops_fwd / ms_b / 1e9, 1),
+           "h100_fwd": h100["fwd"], "h100_bwd": h100["bwd"]}
+    log(f"[sweep] D={hd} L={L} B={B} H={H} pad={pad}%: fwd {row['fwd_tflops']} TFLOPS "
+        f"(H100 {row['h100_fwd']}), bwd {row['bwd_tflops']} (H100 {row['h100_bwd']})")
+    del q, k, v, o, do
+    torch.cuda.empty_cache()
+    return row
+
+
+# Points of the reference grid every default run reports (the "grid" block):
+# D = 128, the chart's L = 4096 (dense and 25 % padding, the shape the
+# reference's published utilisation is read at) and its long end.
+GRID_DEFAULT = [(128, 0, 4096), (128, 25, 4096), (128, 0, 8192), (128, 0, 16384)]
 
 
 # Decode shapes for the split-KV forward (bench.py --decode): bf16, Tq new
@@ -615,6 +621,8 @@ def main():
                     help="with the default c3 config: skip the c4 / c5 padded-vs-dense measurements")
     ap.add_argument("--no-small", action="store_true",
                     help="with the default c3 config: skip the c2 / c2c small-problem step measurements")
+    ap.add_argument("--no-grid", action="store_true",
+                    help="skip the points of the reference benchmark's grid that ride along with c3")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--sweep", action="store_true",
@@ -708,6 +716,15 @@ def main():
                                kernel_ms={n: round(t, 4) for n, t in r["kernel_ms"].items()},
                                workload=workload_name(name, CONFIGS[name]))
 
+    # A few points of the reference benchmark's own grid (fwd and backward-only
+    # TFLOPS, bf16 non-causal, sigmoid_bias = 0, timed as the reference times
+    # them) beside the H100 chart's values: the long end the sweep reaches.
+    grid = []
+    if args.config == "c3" and not args.no_grid:
+        for hd, pad, L in GRID_DEFAULT:
+            torch.cuda.empty_cache()
+            grid.append(sweep_row(hd, pad, L))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(res["cfg"])
@@ -751,6 +768,8 @@ def main():
         line["padded"] = padded
     if small:
         line["small"] = small
+    if grid:
+        line["grid"] = grid
     print(json.dumps(line), flush=True)
 
 
