@@ -221,8 +221,8 @@ def test_two_pass_backward_workspace_size_and_errors():
 def test_python_layer_backward_workspace_policy(monkeypatch):
     """The Python layer passes the whole dS when it fits the limit, else the
     largest whole number of heads, and no workspace (the recompute backward)
-    at D != 128 or when one group's dQ-from-dS grid would have fewer
-    workgroups than the GPU has compute units."""
+    at D != 128 or when one group's dQ-from-dS grid, in workgroups of 256
+    query rows, would have fewer workgroups than the GPU has compute units."""
     lib = _capi.load_library()
     dev = torch.device("cuda", 0)
     monkeypatch.setitem(_capi._CU_COUNT, 0, 256)
@@ -234,9 +234,11 @@ def test_python_layer_backward_workspace_policy(monkeypatch):
     assert per_head == B * 256 * 256 * 2048
     monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", str(full >> 20))
     assert _capi.bwd_workspace_bytes(lib, p, dev) == full
-    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "2303")   # 8 heads of 2 batches: 256 workgroups
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "2303")   # 8 heads of 2 batches
     assert _capi.bwd_workspace_bytes(lib, p, dev) == 8 * per_head
-    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "2047")   # 7 heads: 224 workgroups
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "1024")   # 4 heads: 256 workgroups of 256 rows
+    assert _capi.bwd_workspace_bytes(lib, p, dev) == 4 * per_head
+    monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "1023")   # 3 heads: 192 workgroups
     assert _capi.bwd_workspace_bytes(lib, p, dev) == 0
     monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", "0")
     assert _capi.bwd_workspace_bytes(lib, p, dev) == 0

@@ -185,13 +185,16 @@ def test_baseline_configs_within_2e2(cfg):
         assert err <= 2e-2, (name, err)
 
 
-@pytest.mark.parametrize("B,T,H", [(2, 8192, 16), (1, 16384, 16)], ids=["L8192-two-pass", "L16384-recompute"])
-def test_reference_grid_long_shapes(B, T, H):
+@pytest.mark.parametrize("B,T,H,ws_mb", [(2, 8192, 16, None), (1, 16384, 16, None), (1, 16384, 16, "0")],
+                         ids=["L8192-two-pass", "L16384-two-pass", "L16384-recompute"])
+def test_reference_grid_long_shapes(B, T, H, ws_mb, monkeypatch):
     """The long end of the reference's benchmark grid (bf16 D=128 non-causal,
     sigmoid_bias=0, B = 16384/L, H = 2048/D: benchmarks/benchmark_sigmoid.py:
-    193,202), through the public API.  At L=8192 the backward is the two-pass
-    one in two groups of 8 heads (the 2 GiB workspace cap); at L=16384 a group
-    that fits (4 heads) would not fill the GPU, so the recompute backward runs.
+    193,202), through the public API.  Under the default 2 GiB workspace cap
+    the backward is the two-pass one in head groups: two groups of 8 heads at
+    L=8192, four of 4 at L=16384 (whose dQ-from-dS launches take 256-row
+    workgroups to fill the GPU); with no workspace allowed
+    (SIGATTN_BWD_WORKSPACE_MB=0) the recompute backward runs.
 
     With sigmoid_bias=0 every P is near 1/2 and O sums thousands of them:
     |O| reaches ~150 and one bf16 rounding step there is 1.0, so an absolute
@@ -201,6 +204,8 @@ def test_reference_grid_long_shapes(B, T, H):
     error + tol, tests/test_sigmoid_dense.py:111-114,154-166) and to 2e-2 of
     the slice's largest fp32 magnitude."""
     from oracle.eager import mixed_fwd_bwd
+    if ws_mb is not None:
+        monkeypatch.setenv("SIGATTN_BWD_WORKSPACE_MB", ws_mb)
     D, tol = 128, get_tolerance(torch.bfloat16)
     q, k, v, do = _inputs(B, T, H, D, torch.bfloat16, seed=T)
     for t in (q, k, v):

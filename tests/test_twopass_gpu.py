@@ -216,6 +216,29 @@ def test_head_groups_equal_one_pass(causal):
         assert torch.equal(a, b_)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_small_grid_dq_workgroups_equal_wide_ones(causal):
+    """The D = 128 dQ-from-dS launch takes 512-query workgroups, or 256-query
+    ones when the 512-query grid would leave compute units idle; each query's
+    row accumulates the same products in the same order either way.  B=1
+    T=2048 H=128 with the whole problem's workspace launches 512 wide
+    workgroups; in groups of 32 heads each group's 128 wide workgroups would
+    not fill the GPU, so it runs 256 narrow ones: the same bits."""
+    B, T, H, D = 1, 2048, 128, 128
+    dtype = torch.bfloat16
+    q, k, v, do = _dense_case(B, T, H, D, dtype, seed=13)
+    bias, scale = _scalars(B, T, D)
+    pr = _problem(q, k, v, bias, scale, causal=causal)
+    lib = _capi.load_library()
+    assert lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)) > 0
+    per_head = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr))) // H
+    ref, whole = _both(pr, q, k, do)
+    _assert_twopass_matches(ref, whole, dtype)
+    _, groups = _both(pr, q, k, do, ws_bytes=32 * per_head)
+    for name, a, b_ in zip(("dQ", "dK", "dV"), whole, groups):
+        assert torch.equal(a, b_), name
+
+
 def test_halves_equal_whole():
     """sigattn_bwd_dkdv_ws then sigattn_bwd_dq_ws give sigattn_bwd_ws's bits;
     with less than the whole problem's workspace the halves refuse."""

@@ -1074,15 +1074,24 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_pair_kernel(const KParams p) 
 #endif
 constexpr bool kDqDsNT = SIGATTN_DQDS_NT != 0;
 
+// Waves per SIMD of the kernel's resident workgroups (its register budget).
+template <int D, int NW, int KB, int NST> constexpr int dq_ds_waves_per_simd() {
+  const int occ = 163840 / (NST * (32 * KB * D + NW * 2 * KB * DsLayout::kTileElems) * 2);
+  return occ * NW / 4 > 1 ? occ * NW / 4 : 1;
+}
+
 template <typename T, int D, bool CAUSAL, int NW, int KB, int NST>
-__global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) {
+__global__ __launch_bounds__(64 * NW, (dq_ds_waves_per_simd<D, NW, KB, NST>())) void bwd_dq_ds_kernel(
+    const KParams p) {
   constexpr int BM = 64 * NW, BN = 32 * KB;
   constexpr int NDB = D / 32;
   constexpr int TE = DsLayout::kTileElems;
   constexpr int KI = BN * D / 8 / 64 / NW;  // K-row copy instructions per wave and stage
   constexpr int NI = KI + 4 * KB;           // copy instructions per wave and stage
   constexpr int PF = NST - 1;               // stages in flight ahead of the one computed
-  static_assert(KI >= 1 && (NST - 2) * NI < 64, "stage shape");
+  // Resident workgroups per CU, by the LDS ring's size (160 KB per CU).
+  constexpr int OCC = 163840 / (NST * (BN * D + NW * 2 * KB * TE) * 2);
+  static_assert(KI >= 1 && (NST - 2) * NI < 64 && OCC >= 1, "stage shape");
 
   __shared__ __attribute__((aligned(16))) uint16_t sK[NST][BN * D];
   __shared__ __attribute__((aligned(16))) uint16_t sS[NST][NW * 2 * KB * TE];
@@ -1093,7 +1102,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_dq_ds_kernel(const KParams p) 
   if (p.ragged() && p.B <= 64) {
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
-    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu, 1)
+    const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu, OCC)
                                : WorkOrder::by_stream(wg, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qblk = it.blk;
   } else {
@@ -1341,9 +1350,29 @@ static void bwd_dkdv_t(const KParams &kp, bool causal, bool sm, hipStream_t st) 
 #define SIGATTN_DQDS_NST_128 4
 #endif
 
+// Grids of the D = 128 kernel with fewer 8-wave workgroups than the GPU has
+// compute units (small problems, and long ones whose heads run in groups
+// under the workspace cap) take 4-wave workgroups of 256 query rows with a
+// 3-stage ring (72 KB, two per CU) instead, twice the workgroups on twice
+// the CUs.
+#ifndef SIGATTN_DQDS_SMALL_GRID
+#define SIGATTN_DQDS_SMALL_GRID 1
+#endif
+
 template <typename T, int D>
 static void bwd_dq_ds_t(const KParams &kp, bool causal, hipStream_t st) {
   constexpr int NW128 = SIGATTN_DQDS_NW_128, NST128 = SIGATTN_DQDS_NST_128;
+  if constexpr (D == 128) {
+    const int64_t wide = (int64_t)((kp.Tq + 64 * NW128 - 1) / (64 * NW128)) * kp.B * kp.H;
+    if (SIGATTN_DQDS_SMALL_GRID && NW128 == 8 && wide < kp.ncu) {
+      launch_rows<256>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
+        grid.x += (unsigned)(p.ngap[0] + p.ngap[1]);
+        if (causal) bwd_dq_ds_kernel<T, D, true, 4, 1, 3><<<grid, 256, 0, st>>>(p);
+        else bwd_dq_ds_kernel<T, D, false, 4, 1, 3><<<grid, 256, 0, st>>>(p);
+      });
+      return;
+    }
+  }
   launch_rows<(D == 128 ? 64 * NW128 : 256)>(kp, kp.Tq, [&](const KParams &p, dim3 grid) {
     // D = 128: 8 waves (512 query rows: each K row read serves twice the dS
     // of a 4-wave workgroup; two waves per SIMD), one 32-key block per stage

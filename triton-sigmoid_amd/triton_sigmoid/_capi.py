@@ -295,8 +295,10 @@ def bwd_workspace_limit() -> int:
     return max(mb, 0) << 20
 
 
-# Query rows per workgroup of the D = 128 dQ-from-dS kernel.
-_DQ_DS_ROWS = 512
+# Query rows per workgroup of the D = 128 dQ-from-dS kernel on grids that
+# would not fill the GPU with its 512-row workgroups (the library then
+# launches 256-row ones).
+_DQ_DS_ROWS = 256
 _CU_COUNT: dict = {}
 
 
@@ -313,11 +315,13 @@ def bwd_workspace_bytes(lib, pr: SigattnProblem, device: torch.device) -> int:
 
     The whole problem's dS when it fits bwd_workspace_limit(); otherwise the
     largest whole number of heads that fits, run by the library one group
-    after another.  Groups whose dQ-from-dS grid has fewer workgroups than
-    the GPU has compute units are no faster than the recompute backward
-    (measured at D=128 non-causal: B=1 L=16384 H=16 in groups of 4 heads,
-    128 workgroups, 6.78 ms against 6.76 ms; B=2 L=8192 H=16 in groups of 8
-    heads, 256 workgroups, 3.14 ms against 3.44 ms), so those take it."""
+    after another.  Groups whose dQ-from-dS grid (in workgroups of 256 query
+    rows) has fewer workgroups than the GPU has compute units take the
+    recompute backward instead.  Measured at D=128 bf16 (ms, two-pass in
+    head groups against recompute): non-causal B=1 L=16384 H=16 in groups
+    of 4 heads (256 workgroups) 6.04-6.05 against 6.90-6.91, B=2 L=8192
+    H=16 in groups of 8 3.00-3.02 against 3.49; causal B=1 L=16384 H=16 in
+    groups of 4 3.57-3.59 against 3.56-3.57."""
     if pr.D not in TWO_PASS_HEAD_DIMS:
         return 0
     full = int(lib.sigattn_bwd_workspace_bytes(ctypes.byref(pr)))
