@@ -627,6 +627,8 @@ def main():
                     help="only run a 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference benchmark's L/D/padding grid, beside its published H100 chart")
+    ap.add_argument("--sweep-point", nargs=3, type=int, metavar=("D", "PAD_PCT", "L"),
+                    help="one point of that grid")
     ap.add_argument("--decode", action="store_true",
                     help="split-KV forward at decode shapes (HBM GB/s)")
     ap.add_argument("--ceiling", action="store_true",
@@ -656,8 +658,12 @@ def main():
         print(json.dumps({"metric": "split-KV decode forward: HBM GB/s of K, V, Q, O", "unit": "GB/s",
                           "peak_tbps": HBM_PEAK_TBPS, "rows": rows}), flush=True)
         return
-    if args.sweep:
-        rows = sweep()
+    if args.sweep_point:
+        hd, pad, L = args.sweep_point
+        if hd not in (64, 128) or pad not in (0, 25, 50) or L not in SWEEP_L:
+            sys.exit(f"--sweep-point: D in (64, 128), PAD_PCT in (0, 25, 50), L in {SWEEP_L}")
+    if args.sweep or args.sweep_point:
+        rows = sweep() if args.sweep else [sweep_row(*args.sweep_point)]
         print(json.dumps({"metric": "reference benchmark grid: fwd and bwd-only TFLOPS, bf16 non-causal",
                           "unit": "TFLOPS", "rows": rows}), flush=True)
         return
