@@ -522,8 +522,9 @@ def sweep_row(hd: int, pad: int, L: int) -> dict:
 
 # Points of the reference grid every default run reports (the "grid" block):
 # D = 128, the chart's L = 4096 (dense and 25 % padding, the shape the
-# reference's published utilisation is read at) and its long end.
-GRID_DEFAULT = [(128, 0, 4096), (128, 25, 4096), (128, 0, 8192), (128, 0, 16384)]
+# reference's published utilisation is read at) and its long end, and D = 64
+# at L = 4096.
+GRID_DEFAULT = [(128, 0, 4096), (128, 25, 4096), (128, 0, 8192), (128, 0, 16384), (64, 0, 4096)]
 
 
 # Decode shapes for the split-KV forward (bench.py --decode): bf16, Tq new
