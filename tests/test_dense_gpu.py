@@ -231,52 +231,6 @@ def test_reference_grid_long_shapes(B, T, H, ws_mb, monkeypatch):
             del ro, qq, kk, vv, ref, mixed
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("layout", ["dense", "padded", "packed"])
-def test_d64_wide_forward_equals_narrow(dtype, layout):
-    """Large non-causal D = 64 grids (at least four 256-query items per CU)
-    run the forward with 64-query waves; each query row gets the same
-    products in the same order as with the 32-query waves that smaller grids
-    run, so the whole batch (wide) and each sequence alone (narrow) give the
-    same bits.  One (batch, head) slice is also held to the oracle."""
-    B, T, H, D = 4, 2048, 32, 64
-    q, k, v, _ = _inputs(B, T, H, D, dtype, seed=64)
-    lens = [2048, 1500, 2048, 777] if layout != "dense" else [T] * B
-    if layout == "dense":
-        whole = ts.sigmoid_attention(q, k, v)
-        parts = [ts.sigmoid_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1]) for b in range(B)]
-        got = [whole[b:b + 1] for b in range(B)]
-    elif layout == "padded":
-        sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
-        whole = ts.sigmoid_attention_padded(q, k, v, seq_lens_k=sl, seq_lens_q=sl)
-        parts = [ts.sigmoid_attention_padded(q[b:b + 1], k[b:b + 1], v[b:b + 1], seq_lens_k=sl[b:b + 1],
-                                             seq_lens_q=sl[b:b + 1]) for b in range(B)]
-        got = [whole[b:b + 1] for b in range(B)]
-    else:
-        qp, kp, vp = (torch.cat([t[b, :n] for b, n in enumerate(lens)], 0) for t in (q, k, v))
-        cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=DEV)
-        whole = ts.sigmoid_attention_varlen(qp, kp, vp, cu, cu)
-        parts, got = [], []
-        for b, n in enumerate(lens):
-            one = torch.tensor([0, n], dtype=torch.int32, device=DEV)
-            r = slice(int(cu[b]), int(cu[b + 1]))
-            parts.append(ts.sigmoid_attention_varlen(qp[r], kp[r], vp[r], one, one))
-            got.append(whole[r])
-    for b in range(B):
-        assert torch.equal(got[b], parts[b]), f"batch {b}"
-    # Oracle on batch 1, heads 0-1 (its own length's default bias).
-    n = lens[1]
-    sl1 = torch.tensor([n], dtype=torch.int32)
-    qs, ks, vs = (t[1:2, :n, :2].contiguous() for t in (q, k, v))
-    if layout == "dense":
-        bias = np.array([-math.log(n)], dtype=np.float32).astype(np.float64)
-    else:  # -log(length) in fp32, as the padded and packed APIs compute it
-        bias = (-torch.log(sl1.float())).double().numpy()
-    want, _ = oracle_fwd_bwd(qs, ks, vs, qs, scale=np.float32(1 / math.sqrt(D)), bias=bias, with_bwd=False)
-    o1 = got[1][0, :n, :2] if layout != "packed" else got[1][:, :2]
-    assert_close_to_oracle(o1[None], want, dtype, "O")
-
-
 @pytest.mark.parametrize("causal", [False, True])
 def test_c1_fp32_matches_oracle(causal):
     """fp32 B=2 L=256 H=4 D=64, q/k/v/dO ~ N(0,1)

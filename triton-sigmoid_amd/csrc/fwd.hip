@@ -61,15 +61,13 @@ constexpr bool kFwdCausalPairs = SIGATTN_FWD_CAUSAL_PAIRS != 0;
 #endif
 constexpr int kFwdBhGroup = SIGATTN_FWD_BH_GROUP;
 // Resident workgroups per CU: D = 128 one (128 KB of LDS); D = 64 three (or
-// two with four stages), two with 64-query waves (NCB = 2, whose registers
-// allow two waves per SIMD); D = 32 four (32 KB, at most 128 registers per
-// wave).
-template <int D, int NCB = 1> constexpr int fwd_occupancy() {
-  return D == 64 ? (NCB == 2 || fwd_stages<D>() != 3 ? 2 : 3) : (D == 32 ? 4 : 1);
+// two with four stages); D = 32 four (32 KB, at most 128 registers per wave).
+template <int D> constexpr int fwd_occupancy() {
+  return D == 64 ? (fwd_stages<D>() == 3 ? 3 : 2) : (D == 32 ? 4 : 1);
 }
 
 template <typename T, int D, int NWV, int NCB, bool CAUSAL, bool SCOREMOD>
-__global__ __launch_bounds__(64 * NWV, (fwd_occupancy<D, NCB>())) void fwd_mfma_kernel(const KParams p) {
+__global__ __launch_bounds__(64 * NWV, fwd_occupancy<D>()) void fwd_mfma_kernel(const KParams p) {
   // NWV waves per workgroup (8: two per SIMD), NCB 32-query column blocks each.
   constexpr int QW = 32 * NCB;          // queries per wave
   constexpr int BM = NWV * QW;          // queries per workgroup
@@ -82,11 +80,9 @@ __global__ __launch_bounds__(64 * NWV, (fwd_occupancy<D, NCB>())) void fwd_mfma_
   // Operand read-ahead, in steps.  D = 128: a whole region (16) without
   // score_mod, 8 with it (16 would spill there); measured 2-3 % (8 vs 4) and
   // another 1-2.5 % (16 vs 8) at the headline shapes.  D = 64: 4 (three waves
-  // per SIMD, 168 registers each), 2 with 64-query waves (4 spills past 256
-  // registers); D = 32: 4, a whole region (2 with score_mod, which spills at
-  // four waves per SIMD otherwise).
-  constexpr int LA =
-      D == 128 ? (SCOREMOD ? 8 : 16) : ((D == 32 && SCOREMOD) || (D == 64 && NCB == 2) ? 2 : 4);
+  // per SIMD, 168 registers each); D = 32: 4, a whole region (2 with
+  // score_mod, which spills at four waves per SIMD otherwise).
+  constexpr int LA = D == 128 ? (SCOREMOD ? 8 : 16) : (D == 32 && SCOREMOD ? 2 : 4);
   constexpr int NWD = 8 * NCB;          // packed P words per block
   constexpr int BAR = NSTEP - LA;       // step of the tile barrier in odd regions
   static_assert(NSTEP % LA == 0, "region shape");
@@ -109,7 +105,7 @@ __global__ __launch_bounds__(64 * NWV, (fwd_occupancy<D, NCB>())) void fwd_mfma_
     const auto lq = [&](int i) SIGATTN_INLINE { return p.len_q(i); };
     const auto lk = [&](int i) SIGATTN_INLINE { return p.len_k(i); };
     const WorkItem it = CAUSAL ? WorkOrder::by_level(wg, p.B, p.H, lq, BM, p.nblk, true, p.ncu,
-                                                     fwd_occupancy<D, NCB>())
+                                                     fwd_occupancy<D>())
                                : WorkOrder::by_stream(wg, p.B, p.H, lq, BM, p.nblk, lk);
     b = it.b, h = it.h, qb0 = it.blk;
   } else {
@@ -469,9 +465,9 @@ __global__ __launch_bounds__(64 * NWV, (fwd_occupancy<D, NCB>())) void fwd_mfma_
 #define SIGATTN_FWD_NCB 1
 #endif
 
-template <typename T, int D, int NWV, int NCB>
+template <typename T, int D, int NWV>
 static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
-  constexpr int BM = NWV * 32 * NCB;
+  constexpr int NCB = SIGATTN_FWD_NCB, BM = NWV * 32 * NCB;
   KParams p = kp;
   p.nblk = (p.Tq + BM - 1) / BM;
   // Dense causal problems (the kernel's order when not ragged with B <= 64):
@@ -495,31 +491,9 @@ static void launch_fwd_w(const KParams &kp, bool causal, bool scoremod, hipStrea
 // better on small or ragged (padded) batches.  Measured against two
 // workgroups per CU with a 4-stage ring: 10-20 % faster dense (c4, c5 shapes)
 // and 5-13 % padded.
-// D = 64, large non-causal grids: four waves of 64 queries (NCB = 2, every
-// K / Vᵀ operand read feeding two MFMAs, two workgroups per CU) where the
-// 256-query items number at least four per CU.  Each query row gets the same
-// products in the same order as with 32-query waves, so the results are the
-// same bits.  Measured (forward ms, 32- / 64-query waves, two runs): B=4
-// Lmax=8192 H=12 dense 0.915 / 0.840-0.845, padded 0.210-0.214 /
-// 0.207-0.209; the reference's grid (bf16, B=16384/L, H=32) 6-8 % faster
-// from L=1024 up dense, 3-7 % with 25 % padding; smaller or causal grids
-// lose (B=8 L=2048 H=8 causal dense 0.061-0.063 / 0.064-0.065, padded
-// 0.0375 / 0.0471; B=2 L=1024 H=8 0.0178 / 0.0254), their longest items
-// being twice as long.  0 turns it off.
-#ifndef SIGATTN_FWD_D64_WIDE
-#define SIGATTN_FWD_D64_WIDE 1
-#endif
-
 template <typename T, int D>
 static void launch_fwd_t(const KParams &kp, bool causal, bool scoremod, hipStream_t st) {
-  if constexpr (D == 64 && SIGATTN_FWD_NCB == 1) {
-    const int64_t items = (int64_t)((kp.Tq + 255) / 256) * kp.B * kp.H;
-    if (SIGATTN_FWD_D64_WIDE && !causal && kp.rsplit <= 1 && kp.ncu > 0 && items >= 4 * (int64_t)kp.ncu) {
-      launch_fwd_w<T, D, 4, 2>(kp, causal, scoremod, st);
-      return;
-    }
-  }
-  launch_fwd_w<T, D, (D <= 64 ? 4 : 8) / SIGATTN_FWD_NCB, SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
+  launch_fwd_w<T, D, (D <= 64 ? 4 : 8) / SIGATTN_FWD_NCB>(kp, causal, scoremod, st);
 }
 
 int fwd_rows_per_workgroup(int D) { return (D <= 64 ? 4 : 8) * 32; }
